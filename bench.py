@@ -1,0 +1,215 @@
+"""Benchmark of the encoder forward (BertModel.ForwardBatch) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one forward of the whole batch (embeddings -> 12 layers -> pooled
+vectors) with token ids already resident in HBM.  Prints one JSON line:
+throughput in embeddings/s, the roofline of the dominant kernel (measured with
+HIP events on the library's stream inside the timed steps), the overall MFMA
+utilisation, and the CPU baseline (the oracle, a C restatement of the
+reference CPU path over OpenBLAS) timed on a bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+METRIC = "embeddings/sec/GPU (Nomic-style, b256 s512, fp16) + MFMA util %"
+PEAK_MFMA_TFLOPS = {0: 157.3, 1: 2500.0, 2: 2500.0}  # MI355X dense fp32 / fp16 / bf16
+PEAK_HBM_GBS = 8000.0
+
+
+def _package():
+    name = "longbow_fletcher_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    pkg_dir = ROOT / "longbow-fletcher_amd"
+    spec = importlib.util.spec_from_file_location(name, pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def kernel_work(cfg, lengths, esz):
+    """Algorithmic work per launch of each kernel class: (flops, hbm bytes)."""
+    T = int(lengths.sum())
+    H, I = cfg.hidden, cfg.intermediate
+    Ni = cfg.inter_cols
+    sq = float((lengths.astype(np.float64) ** 2).sum())
+    return {
+        "embed": (0.0, T * H * (2 * esz + esz) + T * 4),
+        "qkv_gemm": (2.0 * T * H * 3 * H, (T * H + 3 * H * H + T * 3 * H) * esz),
+        "attention": (4.0 * sq * H, (T * 3 * H + T * H) * esz),
+        "o_gemm": (2.0 * T * H * H, (T * H * 2 + H * H) * esz),
+        "add_layernorm": (0.0, 3 * T * H * esz),
+        "ffn_up_gemm": (2.0 * T * H * Ni, (T * H + Ni * H + T * I) * esz),
+        "ffn_down_gemm": (2.0 * T * I * H, (T * I + I * H + T * H) * esz),
+        "pool": (0.0, T * H * esz + len(lengths) * H * 4),
+    }
+
+
+def cpu_baseline(fl, cfg, weights, lengths, ids, budget_s):
+    """Times the oracle on whole sequences of the workload until ~budget_s."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(int(cores or 1), 64))
+    oracle.set_threads(cores)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+
+    def run(rows):
+        sub = np.concatenate([ids[starts[r]:starts[r] + lengths[r]] for r in rows])
+        t0 = time.perf_counter()
+        oracle.forward(cfg, weights, sub, lengths[rows])
+        return time.perf_counter() - t0
+
+    t1 = run([0])
+    n = int(max(1, min(len(lengths), budget_s / max(t1, 1e-3))))
+    rows = list(range(n))
+    t = run(rows) if n > 1 else t1
+    return {"value": round(n / t, 3), "unit": "embeddings/s", "cores": cores, "kind": "port",
+            "sample": f"{n} of {len(lengths)} sequences of the same workload "
+                      f"(lengths {int(lengths[rows].min())}-{int(lengths[rows].max())}), "
+                      f"oracle fp32 reference math, OpenBLAS threads = {cores}, {t:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="nomic-b256-s512-f16")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU serving is "
+                                   "independent replicas per device (see DESIGN.md), --gpus must "
+                                   "be 1"}))
+        sys.exit(2)
+
+    fl = _package()
+    if not fl.LIB_PATH.exists():
+        spec = importlib.util.spec_from_file_location("_b", ROOT / "longbow-fletcher_amd/build.py")
+        b = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(b)
+        b.build()
+    synth = fl.synth
+    w = synth.WORKLOADS[a.workload]
+    cfg, lengths = w.cfg, w.lengths()
+    ids = synth.make_ids(lengths)
+    log(f"workload {w.name}: B={len(lengths)} tokens={int(lengths.sum())}")
+    t0 = time.time()
+    weights = synth.make_weights(cfg)
+    log(f"weights generated in {time.time() - t0:.1f}s")
+
+    ctx = fl.Context(0)
+    model = fl.Model(ctx, cfg, dtype=w.dtype,
+                     math=fl.MATH_REFERENCE if w.dtype == fl.F32 else fl.MATH_EXACT)
+    model.load(weights)
+    d_ids = ctx.int32(ids)
+    d_out = ctx.empty((len(lengths), cfg.hidden))
+    ctx.synchronize()
+
+    for i in range(a.warmup):
+        model.forward_device(d_ids, lengths, d_out)
+    ctx.synchronize()
+    log("warmup done")
+
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        model.forward_device(d_ids, lengths, d_out)
+    ctx.synchronize()
+    total = time.perf_counter() - t0
+    ms_step = total * 1000.0 / a.steps
+    value = len(lengths) * a.steps / total
+    log(f"timed {a.steps} steps: {ms_step:.3f} ms/step, {value:.1f} emb/s")
+    nan, bad = model.status()
+
+    esz = 4 if w.dtype == fl.F32 else 2
+    work = kernel_work(cfg, lengths, esz)
+    total_flops = cfg.layers * sum(work[k][0] for k in
+                                   ("qkv_gemm", "attention", "o_gemm", "ffn_up_gemm",
+                                    "ffn_down_gemm"))
+    peak = PEAK_MFMA_TFLOPS[w.dtype]
+    mfma_util = total_flops / (ms_step * 1e-3) / (peak * 1e12)
+
+    roofline, kernels = None, {}
+    if not a.no_profile:
+        model.set_profiling(True)
+        ctx.synchronize()
+        for _ in range(a.steps):
+            model.forward_device(d_ids, lengths, d_out)
+        prof = model.profile()
+        model.set_profiling(False)
+        for name, (ms, cnt) in prof.items():
+            if cnt:
+                avg = ms / cnt
+                fl_, by = work[name]
+                kernels[name] = {"avg_ms": round(avg, 4), "launches": cnt,
+                                 "share": None,
+                                 "tflops": round(fl_ / (avg * 1e-3) / 1e12, 1) if fl_ else None,
+                                 "gbs": round(by / (avg * 1e-3) / 1e9, 1)}
+        tot = sum(prof[n][0] for n in kernels)
+        for n in kernels:
+            kernels[n]["share"] = round(prof[n][0] / tot, 4)
+        dom = max(kernels, key=lambda n: prof[n][0])
+        fl_, by = work[dom]
+        avg_s = kernels[dom]["avg_ms"] * 1e-3
+        if fl_:
+            ach = fl_ / avg_s / 1e12
+            roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1), "peak": peak,
+                        "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None}
+        else:
+            ach = by / avg_s / 1e9
+            roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4),
+                        "traffic": None}
+        log(json.dumps(kernels))
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(fl, cfg, weights, lengths, ids, a.cpu_seconds)
+        log(f"cpu baseline {cpu}")
+
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": {0: "fp32", 1: "fp16", 2: "bf16"}[w.dtype],
+        "data": "synthetic (seeded N(0,0.02) weights, uniform ids in [1000,30000) framed 101/102)",
+        "config": {"workload": w.name, "model": cfg.name, "layers": cfg.layers,
+                   "hidden": cfg.hidden, "heads": cfg.heads, "global_batch": len(lengths),
+                   "seq_len": int(lengths.max()), "tokens": int(lengths.sum()),
+                   "parallelism": "single GPU"},
+        "mfma_util": round(mfma_util, 4),
+        "algorithmic_tflops": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "output_nan": nan, "bad_ids": bad,
+    }
+    print(json.dumps(out), flush=True)
+    model.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,715 @@
+// api.cpp -- C ABI: context, buffers and per-op entry points
+// (the Tensor methods of internal/device/device.go:5-116 on HIP).
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "context.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string& msg) { g_err = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorOutOfMemory ? FL_ERR_OOM : FL_ERR_HIP;
+}
+
+int activate(fl_context* ctx) {
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  return FL_OK;
+}
+
+int device_alloc(fl_context* ctx, size_t bytes, void** out) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  ctx->allocated += (int64_t)bytes;
+  *out = p;
+  return FL_OK;
+}
+
+void device_free(fl_context* ctx, void* p) {
+  if (!p) return;
+  (void)hipFree(p);
+  (void)ctx;
+}
+
+void* workspace(fl_context* ctx, size_t bytes, int* status) {
+  *status = FL_OK;
+  if (bytes <= ctx->ws_size) return ctx->ws;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    *status = hip_fail(e, "hipStreamSynchronize");
+    return nullptr;
+  }
+  if (ctx->ws) {
+    (void)hipFree(ctx->ws);
+    ctx->allocated -= (int64_t)ctx->ws_size;
+    ctx->ws = nullptr;
+    ctx->ws_size = 0;
+  }
+  size_t sz = 1 << 20;
+  while (sz < bytes) sz <<= 1;
+  void* p = nullptr;
+  e = hipMalloc(&p, sz);
+  if (e != hipSuccess) {
+    *status = hip_fail(e, "hipMalloc(workspace)");
+    return nullptr;
+  }
+  ctx->ws = p;
+  ctx->ws_size = sz;
+  ctx->allocated += (int64_t)sz;
+  return p;
+}
+
+const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status) {
+  *status = FL_OK;
+  uint32_t bits;
+  std::memcpy(&bits, &base, 4);
+  auto& t = ctx->rope[{bits, half}];
+  if (t.cap >= max_pos && t.cs) return t.cs;
+  int cap = 64;
+  while (cap < max_pos) cap <<= 1;
+  std::vector<float2> host((size_t)cap * half);
+  const int d = 2 * half;
+  for (int p = 0; p < cap; ++p)
+    for (int i = 0; i < half; ++i) {
+      // cpu_backend.go:790-792 (base parameterised).
+      const double theta = (double)p * std::pow((double)base, -2.0 * (double)i / (double)d);
+      host[(size_t)p * half + i] = make_float2((float)std::cos(theta), (float)std::sin(theta));
+    }
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    *status = hip_fail(e, "hipStreamSynchronize");
+    return nullptr;
+  }
+  if (t.cs) (void)hipFree(t.cs);
+  t.cs = nullptr;
+  t.cap = 0;
+  void* p = nullptr;
+  e = hipMalloc(&p, host.size() * sizeof(float2));
+  if (e != hipSuccess) {
+    *status = hip_fail(e, "hipMalloc(rope)");
+    return nullptr;
+  }
+  e = hipMemcpy(p, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    *status = hip_fail(e, "hipMemcpy(rope)");
+    return nullptr;
+  }
+  t.cs = (float2*)p;
+  t.cap = cap;
+  return t.cs;
+}
+
+}  // namespace fl
+
+using namespace fl;
+
+#define FL_ENTER(ctx)                                                  \
+  if (!(ctx)) return fail(FL_ERR_INVALID, "null context");             \
+  std::lock_guard<std::recursive_mutex> _fl_lock((ctx)->mu);           \
+  do {                                                                 \
+    int _fl_a = activate(ctx);                                         \
+    if (_fl_a) return _fl_a;                                           \
+  } while (0)
+
+#define FL_CHECK_LAUNCH(expr)                                          \
+  do {                                                                 \
+    hipError_t _e = (expr);                                            \
+    if (_e != hipSuccess) return hip_fail(_e, #expr);                  \
+  } while (0)
+
+static bool valid_dtype(int dt) { return dt == FL_F32 || dt == FL_F16 || dt == FL_BF16; }
+
+extern "C" {
+
+const char* fl_last_error(void) { return g_err.c_str(); }
+
+const char* fl_version(void) { return "fletcher-hip 0.1 (gfx950)"; }
+
+int fl_device_count(int* count) {
+  if (!count) return fail(FL_ERR_INVALID, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  *count = n;
+  return FL_OK;
+}
+
+int fl_init(int device, fl_context** out) {
+  if (!out) return fail(FL_ERR_INVALID, "null out");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n) return fail(FL_ERR_INVALID, "device index out of range");
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  auto* ctx = new fl_context();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  void* f = nullptr;
+  e = hipMalloc(&f, 256);
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_fail(e, "hipMalloc(flag)");
+  }
+  ctx->flag = (int*)f;
+  *out = ctx;
+  return FL_OK;
+}
+
+int fl_free_context(fl_context* ctx) {
+  if (!ctx) return FL_OK;
+  {
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->allocs) (void)hipFree(kv.first);
+    ctx->allocs.clear();
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->flag) (void)hipFree(ctx->flag);
+    for (auto& kv : ctx->rope)
+      if (kv.second.cs) (void)hipFree(kv.second.cs);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+  return FL_OK;
+}
+
+int fl_set_device(fl_context* ctx, int device) {
+  if (!ctx) return fail(FL_ERR_INVALID, "null context");
+  std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n) return fail(FL_ERR_INVALID, "device index out of range");
+  if (device == ctx->device) return FL_OK;
+  // Scratch, flag and tables live on the old device: release them there
+  // (buffers from fl_alloc stay where they are).
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) {
+    (void)hipFree(ctx->ws);
+    ctx->allocated -= (int64_t)ctx->ws_size;
+  }
+  if (ctx->flag) (void)hipFree(ctx->flag);
+  for (auto& kv : ctx->rope)
+    if (kv.second.cs) (void)hipFree(kv.second.cs);
+  ctx->ws = nullptr;
+  ctx->ws_size = 0;
+  ctx->flag = nullptr;
+  ctx->rope.clear();
+  (void)hipStreamDestroy(ctx->stream);
+  ctx->stream = nullptr;
+  ctx->device = device;
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+  void* f = nullptr;
+  e = hipMalloc(&f, 256);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(flag)");
+  ctx->flag = (int*)f;
+  return FL_OK;
+}
+
+int fl_synchronize(fl_context* ctx) {
+  FL_ENTER(ctx);
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_vram_usage(fl_context* ctx, int64_t* allocated, int64_t* total) {
+  FL_ENTER(ctx);
+  size_t free_b = 0, total_b = 0;
+  FL_CHECK_LAUNCH(hipMemGetInfo(&free_b, &total_b));
+  if (allocated) *allocated = ctx->allocated;
+  if (total) *total = (int64_t)total_b;
+  return FL_OK;
+}
+
+int fl_get_stream(fl_context* ctx, void** stream) {
+  if (!ctx || !stream) return fail(FL_ERR_INVALID, "null argument");
+  *stream = (void*)ctx->stream;
+  return FL_OK;
+}
+
+int fl_alloc(fl_context* ctx, int64_t bytes, void** out) {
+  FL_ENTER(ctx);
+  if (!out || bytes < 0) return fail(FL_ERR_INVALID, "bad allocation request");
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes > 0 ? (size_t)bytes : 16);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  e = hipMemsetAsync(p, 0, bytes > 0 ? (size_t)bytes : 16, ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "hipMemsetAsync");
+  }
+  ctx->allocs[p] = bytes;
+  ctx->allocated += bytes;
+  *out = p;
+  return FL_OK;
+}
+
+int fl_free(fl_context* ctx, void* ptr) {
+  FL_ENTER(ctx);
+  if (!ptr) return FL_OK;
+  auto it = ctx->allocs.find(ptr);
+  if (it == ctx->allocs.end()) return fail(FL_ERR_INVALID, "pointer not allocated by fl_alloc");
+  // Stream-ordered: earlier work on the buffer completes before it is freed.
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  ctx->allocated -= it->second;
+  ctx->allocs.erase(it);
+  FL_CHECK_LAUNCH(hipFree(ptr));
+  return FL_OK;
+}
+
+int fl_copy_to_device(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
+  FL_ENTER(ctx);
+  if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
+  if (bytes == 0) return FL_OK;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream));
+  // Pageable sources are consumed before return; make that unconditional.
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_copy_to_host(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
+  FL_ENTER(ctx);
+  if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
+  if (bytes == 0) return FL_OK;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_copy_device(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
+  FL_ENTER(ctx);
+  if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
+  if (bytes == 0) return FL_OK;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return FL_OK;
+}
+
+int fl_memset(fl_context* ctx, void* ptr, int value, int64_t bytes) {
+  FL_ENTER(ctx);
+  if (bytes < 0 || (bytes > 0 && !ptr)) return fail(FL_ERR_INVALID, "bad memset");
+  if (bytes == 0) return FL_OK;
+  FL_CHECK_LAUNCH(hipMemsetAsync(ptr, value, (size_t)bytes, ctx->stream));
+  return FL_OK;
+}
+
+int fl_upload_f32(fl_context* ctx, void* dst, int dtype, const float* src, int64_t n,
+                  int rounding) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!dst || !src)))
+    return fail(FL_ERR_INVALID, "bad upload");
+  if (n == 0) return FL_OK;
+  if (dtype == FL_F32) {
+    FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+    return FL_OK;
+  }
+  if (rounding == FL_ROUND_TRUNCATE && dtype != FL_F16)
+    return fail(FL_ERR_UNSUPPORTED, "truncating upload is defined for fp16 only");
+  int st;
+  float* tmp = (float*)workspace(ctx, (size_t)n * 4, &st);
+  if (st) return st;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(tmp, src, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+  FL_CHECK_LAUNCH(launch_cast(tmp, FL_F32, dst, dtype, n, rounding == FL_ROUND_TRUNCATE,
+                              ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_download_f32(fl_context* ctx, float* dst, const void* src, int dtype, int64_t n) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!dst || !src)))
+    return fail(FL_ERR_INVALID, "bad download");
+  if (n == 0) return FL_OK;
+  const void* from = src;
+  if (dtype != FL_F32) {
+    int st;
+    float* tmp = (float*)workspace(ctx, (size_t)n * 4, &st);
+    if (st) return st;
+    FL_CHECK_LAUNCH(launch_cast(src, dtype, tmp, FL_F32, n, 0, ctx->stream));
+    from = tmp;
+  }
+  FL_CHECK_LAUNCH(hipMemcpyAsync(dst, from, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Tensor ops
+// ---------------------------------------------------------------------------
+
+int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, int k,
+            float alpha, const void* a, int lda, const void* b, int ldb, void* c, int ldc) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || m < 0 || n < 0 || k < 0 || !a || !b || !c)
+    return fail(FL_ERR_INVALID, "fl_gemm: bad arguments");
+  if (m == 0 || n == 0) return FL_OK;
+  GemmEpilogue epi;
+  if (!trans_a && alpha == 1.0f) {
+    const void* bnk = b;
+    int ldbn = ldb;
+    if (!trans_b) {
+      // B is [k x n]: pack to [n x k] for the MFMA kernel when the shape allows.
+      if (gemm_nt_supported(dtype, m, n, k, a, lda, a, k, c, ldc, epi) && ldb == n) {
+        int st;
+        void* w = workspace(ctx, (size_t)n * k * dtype_size(dtype), &st);
+        if (st) return st;
+        FL_CHECK_LAUNCH(launch_transpose(dtype, b, k, n, w, 0, ctx->stream));
+        bnk = w;
+        ldbn = k;
+      } else {
+        bnk = nullptr;
+      }
+    }
+    if (bnk && gemm_nt_supported(dtype, m, n, k, a, lda, bnk, ldbn, c, ldc, epi)) {
+      FL_CHECK_LAUNCH(launch_gemm_nt(dtype, a, lda, bnk, ldbn, c, ldc, m, n, k, epi, ctx->stream));
+      return FL_OK;
+    }
+  }
+  FL_CHECK_LAUNCH(launch_gemm_generic(dtype, trans_a, trans_b, m, n, k, alpha, a, lda, b, ldb, c,
+                                      ldc, nullptr, FL_ACT_IDENTITY, FL_MATH_EXACT, ctx->stream));
+  return FL_OK;
+}
+
+int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, const void* w,
+              int w_layout, int out_cols, const void* bias, int act, int math, void* out) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows < 0 || in_cols <= 0 || out_cols <= 0 || !x || !w || !out)
+    return fail(FL_ERR_INVALID, "fl_linear: bad arguments");
+  if (w_layout != FL_W_IN_OUT && w_layout != FL_W_OUT_IN)
+    return fail(FL_ERR_INVALID, "fl_linear: bad weight layout");
+  if (act < FL_ACT_IDENTITY || act > FL_ACT_SWIGLU) return fail(FL_ERR_INVALID, "bad activation");
+  if (act == FL_ACT_SWIGLU && out_cols % 2) return fail(FL_ERR_INVALID, "SwiGLU needs even width");
+  if (rows == 0) return FL_OK;
+  const size_t esz = dtype_size(dtype);
+  // Scratch layout: [fp32 bias][packed W][unfused product]
+  const size_t bias_bytes = bias ? ((size_t)out_cols * 4 + 255) / 256 * 256 : 0;
+  const size_t w_bytes = ((size_t)out_cols * in_cols * esz + 255) / 256 * 256;
+  const bool unfused = act == FL_ACT_SWIGLU || act == FL_ACT_SOFTMAX;
+  const size_t y_bytes = unfused ? (size_t)rows * out_cols * esz : 0;
+  int st;
+  char* ws = (char*)workspace(ctx, bias_bytes + w_bytes + y_bytes, &st);
+  if (st) return st;
+  float* bias32 = nullptr;
+  if (bias) {
+    bias32 = (float*)ws;
+    FL_CHECK_LAUNCH(launch_cast(bias, dtype, bias32, FL_F32, out_cols, 0, ctx->stream));
+  }
+  void* y = unfused ? (void*)(ws + bias_bytes + w_bytes) : out;
+  const int epi_act = (act == FL_ACT_GELU || act == FL_ACT_TANH) ? act : FL_ACT_IDENTITY;
+
+  GemmEpilogue epi;
+  epi.kind = epi_act == FL_ACT_GELU ? EPI_GELU : (epi_act == FL_ACT_TANH ? EPI_TANH : EPI_STORE);
+  epi.math = math;
+  epi.bias = bias32;
+  const void* wnk = w;
+  bool mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, x, in_cols, y,
+                                out_cols, epi);
+  if (mfma && w_layout == FL_W_IN_OUT) {
+    void* pk = ws + bias_bytes;
+    FL_CHECK_LAUNCH(launch_transpose(dtype, w, in_cols, out_cols, pk, 0, ctx->stream));
+    wnk = pk;
+  }
+  if (mfma) mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, wnk, in_cols, y,
+                                     out_cols, epi);
+  if (mfma) {
+    FL_CHECK_LAUNCH(launch_gemm_nt(dtype, x, in_cols, wnk, in_cols, y, out_cols, rows, out_cols,
+                                   in_cols, epi, ctx->stream));
+  } else {
+    const int tb = w_layout == FL_W_OUT_IN;
+    FL_CHECK_LAUNCH(launch_gemm_generic(dtype, 0, tb, rows, out_cols, in_cols, 1.0f, x, in_cols,
+                                        w, tb ? in_cols : out_cols, y, out_cols, bias32, epi_act,
+                                        math, ctx->stream));
+  }
+  if (act == FL_ACT_SWIGLU) {
+    FL_CHECK_LAUNCH(launch_swiglu(dtype, y, rows, out_cols / 2, out, math, ctx->stream));
+  } else if (act == FL_ACT_SOFTMAX) {
+    FL_CHECK_LAUNCH(hipMemcpyAsync(out, y, (size_t)rows * out_cols * esz, hipMemcpyDeviceToDevice,
+                                   ctx->stream));
+    FL_CHECK_LAUNCH(launch_activation(dtype, out, rows, out_cols, FL_ACT_SOFTMAX, math, ctx->stream));
+  }
+  return FL_OK;
+}
+
+int fl_add(fl_context* ctx, int dtype, void* t, const void* other, int64_t n) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!t || !other))) return fail(FL_ERR_INVALID, "fl_add");
+  FL_CHECK_LAUNCH(launch_add(dtype, t, other, n, ctx->stream));
+  return FL_OK;
+}
+
+int fl_add_scalar(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_add_scalar");
+  FL_CHECK_LAUNCH(launch_affine(dtype, t, n, 1.0f, v, ctx->stream));
+  return FL_OK;
+}
+
+int fl_scale(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_scale");
+  if (v == 1.0f) return FL_OK;
+  FL_CHECK_LAUNCH(launch_affine(dtype, t, n, v, 0.0f, ctx->stream));
+  return FL_OK;
+}
+
+int fl_add_bias(fl_context* ctx, int dtype, void* t, int rows, int cols, const void* bias) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !bias)
+    return fail(FL_ERR_INVALID, "fl_add_bias");
+  FL_CHECK_LAUNCH(launch_add_bias(dtype, t, rows, cols, bias, ctx->stream));
+  return FL_OK;
+}
+
+int fl_activation(fl_context* ctx, int dtype, void* t, int rows, int cols, int act, int math) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t) return fail(FL_ERR_INVALID, "fl_activation");
+  if (act != FL_ACT_GELU && act != FL_ACT_TANH && act != FL_ACT_SOFTMAX && act != FL_ACT_IDENTITY)
+    return fail(FL_ERR_INVALID, "fl_activation: unsupported activation");
+  FL_CHECK_LAUNCH(launch_activation(dtype, t, rows, cols, act, math, ctx->stream));
+  return FL_OK;
+}
+
+int fl_layernorm(fl_context* ctx, int dtype, void* t, int rows, int cols, const float* gamma,
+                 const float* beta, float eps) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !gamma || !beta)
+    return fail(FL_ERR_INVALID, "fl_layernorm");
+  if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_layernorm: cols > 4096");
+  FL_CHECK_LAUNCH(launch_layernorm(dtype, t, nullptr, rows, cols, gamma, beta, eps, ctx->stream));
+  return FL_OK;
+}
+
+int fl_add_layernorm(fl_context* ctx, int dtype, void* t, const void* residual, int rows, int cols,
+                     const float* gamma, const float* beta, float eps) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !residual || !gamma || !beta)
+    return fail(FL_ERR_INVALID, "fl_add_layernorm");
+  if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_add_layernorm: cols > 4096");
+  FL_CHECK_LAUNCH(launch_layernorm(dtype, t, residual, rows, cols, gamma, beta, eps, ctx->stream));
+  return FL_OK;
+}
+
+int fl_gather_rows(fl_context* ctx, int dtype, const void* table, int rows, int cols,
+                   const int64_t* idx, int n, void* out) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || rows <= 0 || cols <= 0 || n < 0 || !table || (n > 0 && (!idx || !out)))
+    return fail(FL_ERR_INVALID, "fl_gather_rows");
+  if (n == 0) return FL_OK;
+  std::vector<int> i32(n);
+  for (int i = 0; i < n; ++i) {
+    // cpu_backend.go:500-502 panics on out-of-range indices.
+    if (idx[i] < 0 || idx[i] >= rows) return fail(FL_ERR_INVALID, "Gather index out of bounds");
+    i32[i] = (int)idx[i];
+  }
+  int st;
+  int* d = (int*)workspace(ctx, (size_t)n * 4, &st);
+  if (st) return st;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(d, i32.data(), (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+  FL_CHECK_LAUNCH(launch_gather(dtype, table, cols, d, n, out, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+static int rope_common(fl_context* ctx, int dtype, void* t, const std::vector<int>& pos, int heads,
+                       int head_dim, float base) {
+  if (head_dim % 2) return fail(FL_ERR_INVALID, "RoPE needs an even head_dim");
+  const int rows = (int)pos.size();
+  if (rows == 0) return FL_OK;
+  int maxp = 0;
+  for (int p : pos) maxp = p > maxp ? p : maxp;
+  int st;
+  const float2* cs = rope_table(ctx, base, head_dim / 2, maxp + 1, &st);
+  if (st) return st;
+  int* d = (int*)workspace(ctx, (size_t)rows * 4, &st);
+  if (st) return st;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(d, pos.data(), (size_t)rows * 4, hipMemcpyHostToDevice, ctx->stream));
+  FL_CHECK_LAUNCH(launch_rope(dtype, t, rows, heads, head_dim, heads * head_dim, d, cs, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_rope(fl_context* ctx, int dtype, void* t, int batch, int seq, int heads, int head_dim,
+            float base) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || batch < 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || !t)
+    return fail(FL_ERR_INVALID, "fl_rope");
+  std::vector<int> pos((size_t)batch * seq);
+  for (size_t r = 0; r < pos.size(); ++r) pos[r] = (int)(r % seq);  // cpu_backend.go:783
+  return rope_common(ctx, dtype, t, pos, heads, head_dim, base);
+}
+
+int fl_rope_varlen(fl_context* ctx, int dtype, void* t, const int64_t* lengths, int nseq, int heads,
+                   int head_dim, float base) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || nseq < 0 || heads <= 0 || head_dim <= 0 || !t || (nseq && !lengths))
+    return fail(FL_ERR_INVALID, "fl_rope_varlen");
+  std::vector<int> pos;
+  for (int b = 0; b < nseq; ++b) {
+    if (lengths[b] < 0) return fail(FL_ERR_INVALID, "negative length");
+    for (int64_t i = 0; i < lengths[b]; ++i) pos.push_back((int)i);
+  }
+  return rope_common(ctx, dtype, t, pos, heads, head_dim, base);
+}
+
+// Builds cu_seqlens and the attention work list on the host and runs the
+// kernel that fits the dtype / head size / math mode.
+static int attention_common(fl_context* ctx, int dtype, const void* q, const void* k,
+                            const void* v, void* out, const std::vector<int64_t>& lengths,
+                            int heads, int hidden, float scale, int math) {
+  if (heads <= 0 || hidden <= 0 || hidden % heads) return fail(FL_ERR_INVALID, "bad head split");
+  const int nseq = (int)lengths.size();
+  if (nseq == 0) return FL_OK;
+  const int hd = hidden / heads;
+  std::vector<int> cu(nseq + 1, 0);
+  int max_len = 0;
+  for (int b = 0; b < nseq; ++b) {
+    if (lengths[b] < 0) return fail(FL_ERR_INVALID, "negative length");
+    cu[b + 1] = cu[b] + (int)lengths[b];
+    max_len = (int)lengths[b] > max_len ? (int)lengths[b] : max_len;
+  }
+  const bool fast16 = (dtype == FL_F16 || dtype == FL_BF16) && hd == 64 && math == FL_MATH_EXACT &&
+                      hidden % 8 == 0 && (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0 &&
+                      ((uintptr_t)out & 7) == 0;
+  const bool fast32 = dtype == FL_F32 && hd == 64 && hidden % 4 == 0 &&
+                      (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) == 0;
+  std::vector<AttnWork> work;
+  const int waves = max_len > 64 ? 4 : 2;
+  const int bq = fast16 ? waves * 32 : 64;
+  if (fast16 || fast32) {
+    std::vector<int> order(nseq);
+    for (int b = 0; b < nseq; ++b) order[b] = b;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return lengths[a] > lengths[b]; });
+    for (int b : order)
+      for (int h = 0; h < heads; ++h)
+        for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work.push_back(AttnWork{b, h, q0, 0});
+  }
+  const size_t cu_bytes = ((size_t)(nseq + 1) * 4 + 255) / 256 * 256;
+  int st;
+  char* ws = (char*)workspace(ctx, cu_bytes + work.size() * sizeof(AttnWork), &st);
+  if (st) return st;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(ws, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+  if (!work.empty())
+    FL_CHECK_LAUNCH(hipMemcpyAsync(ws + cu_bytes, work.data(), work.size() * sizeof(AttnWork),
+                                   hipMemcpyHostToDevice, ctx->stream));
+  const int* dcu = (const int*)ws;
+  const AttnWork* dwork = (const AttnWork*)(ws + cu_bytes);
+  if (fast16) {
+    FL_CHECK_LAUNCH(launch_attention_flash(dtype, q, k, v, hidden, out, hidden, dcu, dwork,
+                                           (int)work.size(), scale, waves, ctx->stream));
+  } else if (fast32) {
+    FL_CHECK_LAUNCH(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, hidden,
+                                         (float*)out, hidden, dcu, dwork, (int)work.size(), scale,
+                                         math, ctx->stream));
+  } else {
+    FL_CHECK_LAUNCH(launch_attention_generic(dtype, q, k, v, hidden, out, hidden, dcu, nseq,
+                                             max_len, heads, hd, scale, math, ctx->stream));
+  }
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_attention(fl_context* ctx, int dtype, const void* q, const void* k, const void* v, void* out,
+                 int batch, int seq, int heads, int hidden, float scale, int math) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || batch < 0 || seq < 0 || !q || !k || !v || !out)
+    return fail(FL_ERR_INVALID, "fl_attention");
+  std::vector<int64_t> lengths(batch, seq);
+  return attention_common(ctx, dtype, q, k, v, out, lengths, heads, hidden, scale, math);
+}
+
+int fl_attention_varlen(fl_context* ctx, int dtype, const void* q, const void* k, const void* v,
+                        void* out, const int64_t* lengths, int nseq, int heads, int hidden,
+                        float scale, int math) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || nseq < 0 || !q || !k || !v || !out || (nseq && !lengths))
+    return fail(FL_ERR_INVALID, "fl_attention_varlen");
+  std::vector<int64_t> l(lengths, lengths + nseq);
+  return attention_common(ctx, dtype, q, k, v, out, l, heads, hidden, scale, math);
+}
+
+int fl_cast(fl_context* ctx, const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype) || n < 0 || (n > 0 && (!src || !dst)))
+    return fail(FL_ERR_INVALID, "fl_cast");
+  FL_CHECK_LAUNCH(launch_cast(src, src_dtype, dst, dst_dtype, n, 0, ctx->stream));
+  return FL_OK;
+}
+
+int fl_has_nan(fl_context* ctx, const void* t, int dtype, int64_t n, int* out) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || n < 0 || !out || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_has_nan");
+  FL_CHECK_LAUNCH(hipMemsetAsync(ctx->flag, 0, 4, ctx->stream));
+  FL_CHECK_LAUNCH(launch_has_nan(t, dtype, n, ctx->flag, ctx->stream));
+  int h = 0;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(&h, ctx->flag, 4, hipMemcpyDeviceToHost, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  *out = h != 0;
+  return FL_OK;
+}
+
+int fl_slice(fl_context* ctx, int dtype, const void* src, int rows, int cols, int r0, int r1, int c0,
+             int c1, void* dst) {
+  FL_ENTER(ctx);
+  // cpu_backend.go:288-294 panics on empty slices.
+  if (!valid_dtype(dtype) || !src || !dst || r0 < 0 || c0 < 0 || r1 > rows || c1 > cols ||
+      r1 - r0 <= 0 || c1 - c0 <= 0)
+    return fail(FL_ERR_INVALID, "Slice: invalid dimensions");
+  FL_CHECK_LAUNCH(launch_slice(dtype, src, cols, r0, r1, c0, c1, dst, ctx->stream));
+  return FL_OK;
+}
+
+int fl_mean_pool(fl_context* ctx, int dtype, const void* hidden, int cols, const int64_t* lengths,
+                 int nseq, int l2, float* out) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || cols <= 0 || nseq < 0 || (nseq && (!hidden || !lengths || !out)))
+    return fail(FL_ERR_INVALID, "fl_mean_pool");
+  if (nseq == 0) return FL_OK;
+  std::vector<int> cu(nseq + 1, 0);
+  int max_len = 0;
+  for (int b = 0; b < nseq; ++b) {
+    if (lengths[b] <= 0) return fail(FL_ERR_INVALID, "mean pool needs non-empty sequences");
+    cu[b + 1] = cu[b] + (int)lengths[b];
+    max_len = (int)lengths[b] > max_len ? (int)lengths[b] : max_len;
+  }
+  const int rpc = 64;
+  const size_t chunks = (size_t)(max_len + rpc - 1) / rpc;
+  const size_t cu_bytes = ((size_t)(nseq + 1) * 4 + 255) / 256 * 256;
+  int st;
+  char* ws = (char*)workspace(ctx, cu_bytes + (size_t)nseq * chunks * cols * 4, &st);
+  if (st) return st;
+  FL_CHECK_LAUNCH(hipMemcpyAsync(ws, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+  FL_CHECK_LAUNCH(launch_mean_pool_staged(dtype, hidden, cols, (const int*)ws, nseq, max_len, l2,
+                                          (float*)(ws + cu_bytes), out, nullptr, rpc, ctx->stream));
+  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+}  // extern "C"

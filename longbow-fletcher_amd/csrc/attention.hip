@@ -1,0 +1,491 @@
+// attention.hip -- scaled dot-product attention for gfx950.
+//
+// Backs Tensor.Attention / AttentionVarLen (cpu_backend.go:662-758, 66-132)
+// and the encoder's self-attention (bert.go:610-728).  Inputs are packed rows
+// [T, ld] with head h in columns [h*d, (h+1)*d) (cpu_backend.go:706-718);
+// sequences are given by cu_seqlens, so a uniform batch and a ragged batch
+// take the same path and padding never enters the arithmetic.
+//
+// Flash kernel (16-bit, exact math): computed transposed, S^T = K Q^T and
+// O^T = V^T P^T, so the probabilities leave the first MFMA already in the
+// operand layout of the second one (no cross-lane shuffle of P); only V is
+// transposed, once, while staging it into LDS.  A query column's 64 scores
+// of a key tile live in the 4 lanes {q, q+16, q+32, q+48}, so the row max
+// is a 2-step shuffle.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int ld;   // row stride of q/k/v (elements)
+  int ldo;  // row stride of out
+  const int* cu;
+  const AttnWork* work;
+  float scale;
+};
+
+template <typename T> struct AttnMfma;
+template <> struct AttnMfma<_Float16> {
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                               __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float a, float b) {
+    _Float16 h[2] = {(_Float16)a, (_Float16)b};
+    uint32_t r;
+    __builtin_memcpy(&r, h, 4);
+    return r;
+  }
+};
+template <> struct AttnMfma<__bf16> {
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float a, float b) {
+    __bf16 h[2] = {(__bf16)a, (__bf16)b};
+    uint32_t r;
+    __builtin_memcpy(&r, h, 4);
+    return r;
+  }
+};
+
+// One workgroup = WAVES waves x 32 query rows of one (sequence, head);
+// key/value tiles of 64 rows are double-buffered through LDS.
+template <typename T, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
+  constexpr int D = 64, BKV = 64, NT = WAVES * 64;
+  constexpr int KS = D + 8;    // K tile row stride (halfs)
+  constexpr int VS = BKV + 8;  // V^T tile row stride (halfs)
+  constexpr int CH = BKV * D / 8 / NT;  // 16-byte chunks per thread per tensor
+  static_assert(BKV * D / 8 % NT == 0, "tile/thread mismatch");
+  using V8 = T __attribute__((ext_vector_type(8)));
+  using V4 = T __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) T Ks[2][BKV * KS];
+  __shared__ __attribute__((aligned(16))) T Vt[2][D * VS];
+
+  const AttnWork w = p.work[blockIdx.x];
+  const int s0 = p.cu[w.seq];
+  const int L = p.cu[w.seq + 1] - s0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int hoff = w.head * D;
+  const T* Q = (const T*)p.q;
+  const T* K = (const T*)p.k;
+  const T* V = (const T*)p.v;
+
+  // Q fragments: [q-tile][d-half]; lane holds 8 consecutive d of one query.
+  const int qbase = w.q0 + wave * 32;
+  u32x4_t qf[2][2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qr = qbase + qt * 16 + lrow;
+#pragma unroll
+    for (int ds = 0; ds < 2; ++ds) {
+      if (qr < L)
+        qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + lgrp * 8);
+      else
+        qf[qt][ds] = u32x4_t{0, 0, 0, 0};
+    }
+  }
+
+  u32x4_t rk[CH], rv[CH];
+  auto gload = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NT, row = c >> 3, col = (c & 7) * 8;
+      const int key = kv0 + row;
+      if (key < L) {
+        const size_t off = (size_t)(s0 + key) * p.ld + hoff + col;
+        rk[i] = *(const u32x4_t*)(K + off);
+        rv[i] = *(const u32x4_t*)(V + off);
+      } else {
+        rk[i] = u32x4_t{0, 0, 0, 0};
+        rv[i] = u32x4_t{0, 0, 0, 0};
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NT, row = c >> 3, col = (c & 7) * 8;
+      *(u32x4_t*)(&Ks[buf][row * KS + col]) = rk[i];
+      const V8 e = __builtin_bit_cast(V8, rv[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[buf][(col + j) * VS + row] = e[j];
+    }
+  };
+
+  float4_t o[4][2];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.f, 0.f};
+  const float c = p.scale * 1.4426950408889634f;
+
+  const int ntiles = (L + BKV - 1) / BKV;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1;
+    const int kv0 = it * BKV;
+    if (it + 1 < ntiles) gload(kv0 + BKV);
+
+    // S^T tiles: [key-tile][q-tile]
+    float4_t s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+      s[kt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < 2; ++ds) {
+        const u32x4_t kf = *(const u32x4_t*)(&Ks[cur][(kt * 16 + lrow) * KS + ds * 32 + lgrp * 8]);
+        AttnMfma<T>::mma(s[kt][0], kf, qf[0][ds]);
+        AttnMfma<T>::mma(s[kt][1], kf, qf[1][ds]);
+      }
+    }
+    if (kv0 + BKV > L) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kv0 + kt * 16 + lgrp * 4 + i >= L) {
+            s[kt][0][i] = -INFINITY;
+            s[kt][1][i] = -INFINITY;
+          }
+    }
+
+    u32x4_t pf[2][2];  // [key-step][q-tile] P^T operand
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float mx = s[0][qt][0];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][qt][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[qt], mx);
+      const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
+      const float mc = m_new * c;
+      m_run[qt] = m_new;
+      float lsum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i], c, -mc));
+          s[kt][qt][i] = e;
+          lsum += e;
+        }
+      l_run[qt] = l_run[qt] * alpha + lsum;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        pf[ks][qt][0] = AttnMfma<T>::pack2(s[2 * ks][qt][0], s[2 * ks][qt][1]);
+        pf[ks][qt][1] = AttnMfma<T>::pack2(s[2 * ks][qt][2], s[2 * ks][qt][3]);
+        pf[ks][qt][2] = AttnMfma<T>::pack2(s[2 * ks + 1][qt][0], s[2 * ks + 1][qt][1]);
+        pf[ks][qt][3] = AttnMfma<T>::pack2(s[2 * ks + 1][qt][2], s[2 * ks + 1][qt][3]);
+      }
+    }
+
+    // O^T += V^T P^T
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const T* vrow = &Vt[cur][(dt * 16 + lrow) * VS + ks * 32 + lgrp * 4];
+        const u32x2_t lo = *(const u32x2_t*)vrow;
+        const u32x2_t hi = *(const u32x2_t*)(vrow + 16);
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
+        AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
+      }
+    }
+
+    if (it + 1 < ntiles) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  T* out = (T*)p.out;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float l = l_run[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.0f / l;
+    const int qr = qbase + qt * 16 + lrow;
+    if (qr >= L) continue;
+    T* orow = out + (size_t)(s0 + qr) * p.ldo + hoff + lgrp * 4;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      V4 h;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h[i] = (T)(o[dt][qt][i] * inv);
+      *(V4*)(orow + dt * 16) = h;
+    }
+  }
+}
+
+hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
+                                  int ldqkv, void* out, int ldo, const int* cu_seqlens,
+                                  const AttnWork* work, int n_work, float scale, int waves,
+                                  hipStream_t stream) {
+  if (n_work <= 0) return hipSuccess;
+  AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale};
+  dim3 grid(n_work);
+  if (dtype == F16) {
+    if (waves == 2)
+      hipLaunchKernelGGL((attn_flash_kernel<_Float16, 2>), grid, dim3(128), 0, stream, p);
+    else
+      hipLaunchKernelGGL((attn_flash_kernel<_Float16, 4>), grid, dim3(256), 0, stream, p);
+  } else if (dtype == BF16) {
+    if (waves == 2)
+      hipLaunchKernelGGL((attn_flash_kernel<__bf16, 2>), grid, dim3(128), 0, stream, p);
+    else
+      hipLaunchKernelGGL((attn_flash_kernel<__bf16, 4>), grid, dim3(256), 0, stream, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fp32 two-pass attention (head_dim 64).  Pass 1 finds the exact row max of
+// scale*QK^T; pass 2 evaluates ExpFast(score - max) (MATH_REFERENCE, the
+// reference's SoftmaxFast, simd.go:78-100) or exp, accumulates P V with fp32
+// MFMA and divides by the sum.  An online rescale cannot reproduce ExpFast,
+// whose products are not exponentials of sums, hence the second pass.
+// Workgroup = 4 waves x 16 queries; key tiles of 32 rows.
+// ---------------------------------------------------------------------------
+template <int MATH>
+__global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
+  constexpr int D = 64, BKV = 32, S = D + 4;
+  __shared__ __attribute__((aligned(16))) float Ks[BKV * S];
+  __shared__ __attribute__((aligned(16))) float Vs[BKV * S];
+
+  const AttnWork w = p.work[blockIdx.x];
+  const int s0 = p.cu[w.seq];
+  const int L = p.cu[w.seq + 1] - s0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int hoff = w.head * D;
+  const float* Q = (const float*)p.q;
+  const float* K = (const float*)p.k;
+  const float* V = (const float*)p.v;
+  const float scale = p.scale;
+
+  const int qr = w.q0 + wave * 16 + lrow;
+  // Chunk dc covers d in [16*dc, 16*dc+16); lane group g holds d = 16*dc + 4g + j.
+  u32x4_t qf[4];
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc) {
+    if (qr < L)
+      qf[dc] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + dc * 16 + lgrp * 4);
+    else
+      qf[dc] = u32x4_t{0, 0, 0, 0};
+  }
+
+  auto load_tile = [&](int kv0, bool with_v) {
+    for (int c = tid; c < BKV * D / 4; c += 256) {
+      const int row = c >> 4, col = (c & 15) * 4;
+      const int key = kv0 + row;
+      u32x4_t kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      if (key < L) {
+        const size_t off = (size_t)(s0 + key) * p.ld + hoff + col;
+        kk = *(const u32x4_t*)(K + off);
+        if (with_v) vv = *(const u32x4_t*)(V + off);
+      }
+      *(u32x4_t*)(&Ks[row * S + col]) = kk;
+      if (with_v) *(u32x4_t*)(&Vs[row * S + col]) = vv;
+    }
+  };
+  auto scores = [&](float4_t (&s)[2]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < 4; ++dc) {
+        const u32x4_t kf = *(const u32x4_t*)(&Ks[(kt * 16 + lrow) * S + dc * 16 + lgrp * 4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, kf[j]),
+                                                       __builtin_bit_cast(float, qf[dc][j]),
+                                                       s[kt], 0, 0, 0);
+      }
+    }
+  };
+
+  const int ntiles = (L + BKV - 1) / BKV;
+  // Pass 1: exact row max of the scaled scores.
+  float mx = -INFINITY;
+  for (int it = 0; it < ntiles; ++it) {
+    const int kv0 = it * BKV;
+    load_tile(kv0, false);
+    __syncthreads();
+    float4_t s[2];
+    scores(s);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (kv0 + kt * 16 + lgrp * 4 + i < L) mx = fmaxf(mx, s[kt][i] * scale);
+    __syncthreads();
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+
+  // Pass 2: probabilities and P V.
+  float4_t o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  for (int it = 0; it < ntiles; ++it) {
+    const int kv0 = it * BKV;
+    load_tile(kv0, true);
+    __syncthreads();
+    float4_t s[2];
+    scores(s);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float e = 0.f;
+        if (kv0 + kt * 16 + lgrp * 4 + i < L) {
+          const float sc = s[kt][i] * scale;
+          if constexpr (MATH == MATH_REFERENCE) e = exp_fast_ref(sc - mx);
+          else e = expf(sc - mx);
+        }
+        s[kt][i] = e;
+        lsum += e;
+      }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float vv = Vs[(kt * 16 + lgrp * 4 + j) * S + dt * 16 + lrow];
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, s[kt][j], o[dt], 0, 0, 0);
+        }
+    __syncthreads();
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float inv = 1.0f / lsum;
+  if (qr < L) {
+    float* orow = (float*)p.out + (size_t)(s0 + qr) * p.ldo + hoff + lgrp * 4;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      float4_t r = o[dt] * inv;
+      *(float4_t*)(orow + dt * 16) = r;
+    }
+  }
+}
+
+hipError_t launch_attention_f32(const float* q, const float* k, const float* v, int ldqkv,
+                                float* out, int ldo, const int* cu_seqlens,
+                                const AttnWork* work, int n_work, float scale, int math,
+                                hipStream_t stream) {
+  if (n_work <= 0) return hipSuccess;
+  AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale};
+  if (math == MATH_REFERENCE)
+    hipLaunchKernelGGL(attn_f32_kernel<MATH_REFERENCE>, dim3(n_work), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(attn_f32_kernel<MATH_EXACT>, dim3(n_work), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Generic attention: one thread per (sequence, head, query row), any
+// head_dim <= 256; three sweeps over the keys (max, sum, weighted V).
+// ---------------------------------------------------------------------------
+template <typename T, int MATH>
+__global__ void __launch_bounds__(128)
+attn_generic_kernel(const T* q, const T* k, const T* v, int ld, T* out, int ldo, const int* cu,
+                    int max_len, int heads, int hd, float scale) {
+  const int seq = blockIdx.y, h = blockIdx.z;
+  const int qi = blockIdx.x * blockDim.x + threadIdx.x;
+  const int s0 = cu[seq], L = cu[seq + 1] - s0;
+  if (qi >= L) return;
+  (void)max_len;
+  (void)heads;
+  const T* qrow = q + (size_t)(s0 + qi) * ld + h * hd;
+  float mx = -INFINITY;
+  for (int j = 0; j < L; ++j) {
+    const T* krow = k + (size_t)(s0 + j) * ld + h * hd;
+    float acc = 0.f;
+    for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
+    mx = fmaxf(mx, acc * scale);
+  }
+  float sum = 0.f;
+  for (int j = 0; j < L; ++j) {
+    const T* krow = k + (size_t)(s0 + j) * ld + h * hd;
+    float acc = 0.f;
+    for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
+    sum += MATH == MATH_REFERENCE ? exp_fast_ref(acc * scale - mx) : expf(acc * scale - mx);
+  }
+  const float inv = 1.0f / sum;
+  T* orow = out + (size_t)(s0 + qi) * ldo + h * hd;
+  for (int d0 = 0; d0 < hd; d0 += 32) {
+    float o[32];
+    const int dn = min(32, hd - d0);
+    for (int d = 0; d < 32; ++d) o[d] = 0.f;
+    for (int j = 0; j < L; ++j) {
+      const T* krow = k + (size_t)(s0 + j) * ld + h * hd;
+      const T* vrow = v + (size_t)(s0 + j) * ld + h * hd;
+      float acc = 0.f;
+      for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
+      const float pr =
+          (MATH == MATH_REFERENCE ? exp_fast_ref(acc * scale - mx) : expf(acc * scale - mx)) * inv;
+      for (int d = 0; d < dn; ++d) o[d] += pr * to_f(vrow[d0 + d]);
+    }
+    for (int d = 0; d < dn; ++d) orow[d0 + d] = from_f<T>(o[d]);
+  }
+}
+
+template <typename T>
+static hipError_t gen_typed(const void* q, const void* k, const void* v, int ld, void* out,
+                            int ldo, const int* cu, int nseq, int max_len, int heads, int hd,
+                            float scale, int math, hipStream_t s) {
+  dim3 grid((max_len + 127) / 128, nseq, heads), block(128);
+  if (math == MATH_REFERENCE)
+    hipLaunchKernelGGL((attn_generic_kernel<T, MATH_REFERENCE>), grid, block, 0, s, (const T*)q,
+                       (const T*)k, (const T*)v, ld, (T*)out, ldo, cu, max_len, heads, hd,
+                       scale);
+  else
+    hipLaunchKernelGGL((attn_generic_kernel<T, MATH_EXACT>), grid, block, 0, s, (const T*)q,
+                       (const T*)k, (const T*)v, ld, (T*)out, ldo, cu, max_len, heads, hd,
+                       scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_generic(int dtype, const void* q, const void* k, const void* v,
+                                    int ldqkv, void* out, int ldo, const int* cu_seqlens,
+                                    int nseq, int max_len, int heads, int head_dim, float scale,
+                                    int math, hipStream_t stream) {
+  if (nseq <= 0 || max_len <= 0) return hipSuccess;
+  switch (dtype) {
+    case F32:
+      return gen_typed<float>(q, k, v, ldqkv, out, ldo, cu_seqlens, nseq, max_len, heads,
+                              head_dim, scale, math, stream);
+    case F16:
+      return gen_typed<_Float16>(q, k, v, ldqkv, out, ldo, cu_seqlens, nseq, max_len, heads,
+                                 head_dim, scale, math, stream);
+    case BF16:
+      return gen_typed<__bf16>(q, k, v, ldqkv, out, ldo, cu_seqlens, nseq, max_len, heads,
+                               head_dim, scale, math, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fl

@@ -1,0 +1,58 @@
+// context.hpp -- the fl_context behind the C ABI (internal, host only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/fletcher_hip.h"
+
+namespace fl {
+
+// Thread-local message for fl_last_error().
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+}  // namespace fl
+
+struct fl_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex mu;
+  std::unordered_map<void*, int64_t> allocs;  // buffers handed out by fl_alloc
+  int64_t allocated = 0;
+
+  // Grow-only scratch for per-op temporaries (stream-ordered reuse).
+  void* ws = nullptr;
+  size_t ws_size = 0;
+  int* flag = nullptr;  // 4-byte device flag (HasNaN)
+
+  // RoPE (cos, sin) tables keyed by (base bits, half dim); capacity in positions.
+  struct RopeTable {
+    float2* cs = nullptr;
+    int cap = 0;
+  };
+  std::map<std::pair<uint32_t, int>, RopeTable> rope;
+};
+
+namespace fl {
+
+inline size_t dtype_size(int dt) { return dt == FL_F32 ? 4 : 2; }
+
+// Makes ctx current on the calling thread (cgo calls land on arbitrary OS threads).
+int activate(fl_context* ctx);
+// Returns scratch of at least `bytes` (synchronises the stream when it grows).
+void* workspace(fl_context* ctx, size_t bytes, int* status);
+// Device-side (cos, sin) table for positions [0, max_pos) (float64 angles,
+// cpu_backend.go:790-792 with the base as a parameter).
+const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status);
+int device_alloc(fl_context* ctx, size_t bytes, void** out);
+void device_free(fl_context* ctx, void* p);
+
+}  // namespace fl

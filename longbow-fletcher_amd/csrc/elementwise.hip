@@ -1,0 +1,395 @@
+// elementwise.hip -- memory-bound Tensor ops (device.go:44-116) and pooling.
+//
+// Add / Scale / AddScalar / AddBias / Gelu / Tanh / Softmax / Cast / HasNaN /
+// Gather / Slice / ApplyRoPE, plus the masked mean-pool (+L2) and CLS gather
+// that turn last hidden states into one vector per sequence.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+static inline dim3 grid_for(int64_t n, int per_block = 256 * 4) {
+  int64_t g = (n + per_block - 1) / per_block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return dim3((unsigned)g);
+}
+
+#define FL_GRID_STRIDE(i, n) \
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < (n); i += (int64_t)gridDim.x * blockDim.x)
+
+template <typename T>
+__global__ void add_kernel(T* t, const T* o, int64_t n) {
+#pragma clang fp contract(off)
+  FL_GRID_STRIDE(i, n) t[i] = from_f<T>(to_f(t[i]) + to_f(o[i]));
+}
+
+template <typename T>
+__global__ void affine_kernel(T* t, int64_t n, float mul, float add) {
+#pragma clang fp contract(off)
+  FL_GRID_STRIDE(i, n) {
+    float v = to_f(t[i]);
+    if (mul != 1.0f) v = v * mul;
+    if (add != 0.0f) v = v + add;
+    t[i] = from_f<T>(v);
+  }
+}
+
+template <typename T>
+__global__ void add_bias_kernel(T* t, int rows, int cols, const T* bias) {
+#pragma clang fp contract(off)
+  const int64_t n = (int64_t)rows * cols;
+  FL_GRID_STRIDE(i, n) t[i] = from_f<T>(to_f(t[i]) + to_f(bias[i % cols]));
+}
+
+template <typename T, int ACT, int MATH>
+__global__ void act_kernel(T* t, int64_t n) {
+  FL_GRID_STRIDE(i, n) {
+    const float v = to_f(t[i]);
+    t[i] = from_f<T>(ACT == ACT_GELU ? gelu_m<MATH>(v) : tanh_m<MATH>(v));
+  }
+}
+
+// Row softmax, one wave per row.  MATH_REFERENCE is SoftmaxFast
+// (simd.go:78-100): ExpFast(v - max), sum, times 1/sum.
+template <typename T, int MATH>
+__global__ void __launch_bounds__(256) softmax_kernel(T* t, int rows, int cols) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  T* r = t + (size_t)row * cols;
+  float mx = -INFINITY;
+  for (int j = lane; j < cols; j += 64) mx = fmaxf(mx, to_f(r[j]));
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) {
+    const float v = to_f(r[j]);
+    s += MATH == MATH_REFERENCE ? exp_fast_ref(v - mx) : expf(v - mx);
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  for (int j = lane; j < cols; j += 64) {
+    const float v = to_f(r[j]);
+    const float e = MATH == MATH_REFERENCE ? exp_fast_ref(v - mx) : expf(v - mx);
+    r[j] = from_f<T>(e * inv);
+  }
+}
+
+// SwiGLU over an unfused [rows, 2I] product (cpu_backend.go:636-654).
+template <typename T, int MATH>
+__global__ void swiglu_kernel(const T* in, int rows, int inter, T* out) {
+  const int64_t n = (int64_t)rows * inter;
+  FL_GRID_STRIDE(i, n) {
+    const int64_t r = i / inter, c = i % inter;
+    const float g = to_f(in[r * 2 * inter + c]);
+    const float u = to_f(in[r * 2 * inter + inter + c]);
+    out[i] = from_f<T>(silu_m<MATH>(g) * u);
+  }
+}
+
+// Float32ToFloat16 of utils.go:13-72 (truncating; flush below 2^-14; clamp).
+__device__ inline uint16_t f32_to_f16_ref(float f) {
+  const uint32_t bits = __float_as_uint(f);
+  if (isnan(f)) return 0x7E00;
+  if (isinf(f)) return f > 0 ? 0x7C00 : 0xFC00;
+  if (f > 65504.0f) f = 65504.0f;
+  else if (f < -65504.0f) f = -65504.0f;
+  const float a = fabsf(f);
+  if (a < 6.10351562e-5f && a > 0.f) return f < 0 ? 0x8000 : 0x0000;
+  const uint32_t b = __float_as_uint(f);
+  (void)bits;
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const int e = (int)((b >> 23) & 0xFF) - 127 + 15;
+  const uint32_t frac = (b >> 13) & 0x3FFu;
+  if (e >= 0x1F) return (uint16_t)(sign | 0x7BFFu);
+  if (e <= 0) return (uint16_t)sign;
+  return (uint16_t)(sign | ((uint32_t)e << 10) | frac);
+}
+
+template <typename S, typename D>
+__global__ void cast_kernel(const S* src, D* dst, int64_t n) {
+  FL_GRID_STRIDE(i, n) dst[i] = from_f<D>(to_f(src[i]));
+}
+
+__global__ void cast_f32_f16_ref_kernel(const float* src, uint16_t* dst, int64_t n) {
+  FL_GRID_STRIDE(i, n) dst[i] = f32_to_f16_ref(src[i]);
+}
+
+template <typename T>
+__global__ void has_nan_kernel(const T* t, int64_t n, int* flag) {
+  bool bad = false;
+  FL_GRID_STRIDE(i, n) {
+    const float v = to_f(t[i]);
+    bad |= !isfinite(v);
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+template <typename T>
+__global__ void gather_kernel(const T* table, int cols, const int* idx, int n, T* out) {
+  const int64_t total = (int64_t)n * cols;
+  FL_GRID_STRIDE(i, total) {
+    const int64_t r = i / cols, c = i % cols;
+    out[i] = table[(size_t)idx[r] * cols + c];
+  }
+}
+
+template <typename T>
+__global__ void slice_kernel(const T* src, int cols, int r0, int c0, int rows_out, int cols_out,
+                             T* dst) {
+  const int64_t total = (int64_t)rows_out * cols_out;
+  FL_GRID_STRIDE(i, total) {
+    const int64_t r = i / cols_out, c = i % cols_out;
+    dst[i] = src[(size_t)(r0 + r) * cols + c0 + c];
+  }
+}
+
+// RoPE (cpu_backend.go:760-805): pairs (i, i + d/2) of each head rotated by
+// the (cos, sin) of theta = pos * base^(-2i/d), table computed in float64.
+template <typename T>
+__global__ void rope_kernel(T* t, int rows, int heads, int hd, int ld, const int* pos,
+                            const float2* cs) {
+#pragma clang fp contract(off)
+  const int half = hd / 2;
+  const int64_t total = (int64_t)rows * heads * half;
+  FL_GRID_STRIDE(i, total) {
+    const int64_t r = i / ((int64_t)heads * half);
+    const int rem = (int)(i % ((int64_t)heads * half));
+    const int h = rem / half, j = rem % half;
+    T* x = t + (size_t)r * ld + h * hd;
+    const float2 c = cs[(size_t)pos[r] * half + j];
+    const float x1 = to_f(x[j]), x2 = to_f(x[j + half]);
+    x[j] = from_f<T>(x1 * c.x - x2 * c.y);
+    x[j + half] = from_f<T>(x1 * c.y + x2 * c.x);
+  }
+}
+
+// Masked mean-pool, stage 1: per (sequence, row chunk) column sums into
+// part[seq][chunk][cols] (deterministic, no atomics).
+template <typename T>
+__global__ void __launch_bounds__(256)
+pool_partial_kernel(const T* hidden, int cols, const int* cu, int rows_per_chunk, int max_chunks,
+                    float* part) {
+  const int seq = blockIdx.y, chunk = blockIdx.x;
+  const int s0 = cu[seq], L = cu[seq + 1] - s0;
+  const int r0 = chunk * rows_per_chunk;
+  float* dst = part + ((size_t)seq * max_chunks + chunk) * cols;
+  const int r1 = min(L, r0 + rows_per_chunk);
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    float acc = 0.f;
+    for (int r = r0; r < r1; ++r) acc += to_f(hidden[(size_t)(s0 + r) * cols + c]);
+    dst[c] = acc;
+  }
+}
+
+// Stage 2: sum chunks, divide by L, optional L2 normalisation, NaN flag.
+__global__ void __launch_bounds__(256)
+pool_final_kernel(const float* part, int cols, const int* cu, int rows_per_chunk, int max_chunks,
+                  int l2, float* out, int* nan_flag) {
+  __shared__ float red[4];
+  const int seq = blockIdx.x;
+  const int L = cu[seq + 1] - cu[seq];
+  const int nchunks = (L + rows_per_chunk - 1) / rows_per_chunk;
+  float* orow = out + (size_t)seq * cols;
+  float ss = 0.f;
+  bool bad = false;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    float acc = 0.f;
+    for (int k = 0; k < nchunks; ++k) acc += part[((size_t)seq * max_chunks + k) * cols + c];
+    const float m = acc / (float)L;
+    orow[c] = m;
+    ss += m * m;
+  }
+  if (l2) {
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    float tot = 0.f;
+    for (int w = 0; w < nw; ++w) tot += red[w];
+    const float inv = 1.0f / fmaxf(sqrtf(tot), 1e-12f);
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+      const float v = orow[c] * inv;
+      orow[c] = v;
+      bad |= !isfinite(v);
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) bad |= !isfinite(orow[c]);
+  }
+  if (nan_flag && __any(bad) && (threadIdx.x & 63) == 0) atomicOr(nan_flag, 1);
+}
+
+template <typename T>
+__global__ void gather_cls_kernel(const T* hidden, int cols, const int* cu, int nseq,
+                                  float* out) {
+  const int64_t total = (int64_t)nseq * cols;
+  FL_GRID_STRIDE(i, total) {
+    const int64_t s = i / cols, c = i % cols;
+    out[i] = to_f(hidden[(size_t)cu[s] * cols + c]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+#define FL_DISPATCH(dtype, T, ...)              \
+  switch (dtype) {                              \
+    case F32: {                                 \
+      using T = float;                          \
+      __VA_ARGS__;                              \
+      break;                                    \
+    }                                           \
+    case F16: {                                 \
+      using T = _Float16;                       \
+      __VA_ARGS__;                              \
+      break;                                    \
+    }                                           \
+    case BF16: {                                \
+      using T = __bf16;                         \
+      __VA_ARGS__;                              \
+      break;                                    \
+    }                                           \
+    default: return hipErrorInvalidValue;       \
+  }
+
+hipError_t launch_add(int dtype, void* t, const void* o, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(add_kernel<T>, grid_for(n), dim3(256), 0, s, (T*)t,
+                                           (const T*)o, n));
+  return hipGetLastError();
+}
+
+hipError_t launch_affine(int dtype, void* t, int64_t n, float mul, float add, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(affine_kernel<T>, grid_for(n), dim3(256), 0, s, (T*)t,
+                                           n, mul, add));
+  return hipGetLastError();
+}
+
+hipError_t launch_add_bias(int dtype, void* t, int rows, int cols, const void* bias,
+                           hipStream_t s) {
+  const int64_t n = (int64_t)rows * cols;
+  if (n <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(add_bias_kernel<T>, grid_for(n), dim3(256), 0, s,
+                                           (T*)t, rows, cols, (const T*)bias));
+  return hipGetLastError();
+}
+
+hipError_t launch_activation(int dtype, void* t, int rows, int cols, int act, int math,
+                             hipStream_t s) {
+  const int64_t n = (int64_t)rows * cols;
+  if (n <= 0) return hipSuccess;
+  const bool ref = math == MATH_REFERENCE;
+  if (act == ACT_SOFTMAX) {
+    dim3 g((rows + 3) / 4);
+    FL_DISPATCH(dtype, T,
+                if (ref) hipLaunchKernelGGL((softmax_kernel<T, MATH_REFERENCE>), g, dim3(256), 0,
+                                            s, (T*)t, rows, cols);
+                else hipLaunchKernelGGL((softmax_kernel<T, MATH_EXACT>), g, dim3(256), 0, s,
+                                        (T*)t, rows, cols));
+  } else if (act == ACT_GELU) {
+    FL_DISPATCH(dtype, T,
+                if (ref) hipLaunchKernelGGL((act_kernel<T, ACT_GELU, MATH_REFERENCE>), grid_for(n),
+                                            dim3(256), 0, s, (T*)t, n);
+                else hipLaunchKernelGGL((act_kernel<T, ACT_GELU, MATH_EXACT>), grid_for(n),
+                                        dim3(256), 0, s, (T*)t, n));
+  } else if (act == ACT_TANH) {
+    FL_DISPATCH(dtype, T,
+                if (ref) hipLaunchKernelGGL((act_kernel<T, ACT_TANH, MATH_REFERENCE>), grid_for(n),
+                                            dim3(256), 0, s, (T*)t, n);
+                else hipLaunchKernelGGL((act_kernel<T, ACT_TANH, MATH_EXACT>), grid_for(n),
+                                        dim3(256), 0, s, (T*)t, n));
+  } else if (act != ACT_IDENTITY) {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(int dtype, const void* in, int rows, int inter, void* out, int math,
+                         hipStream_t s) {
+  const int64_t n = (int64_t)rows * inter;
+  if (n <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T,
+              if (math == MATH_REFERENCE) hipLaunchKernelGGL((swiglu_kernel<T, MATH_REFERENCE>),
+                                                             grid_for(n), dim3(256), 0, s,
+                                                             (const T*)in, rows, inter, (T*)out);
+              else hipLaunchKernelGGL((swiglu_kernel<T, MATH_EXACT>), grid_for(n), dim3(256), 0,
+                                      s, (const T*)in, rows, inter, (T*)out));
+  return hipGetLastError();
+}
+
+hipError_t launch_cast(const void* src, int sdt, void* dst, int ddt, int64_t n, int truncate_ref,
+                       hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (truncate_ref) {
+    if (sdt != F32 || ddt != F16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(cast_f32_f16_ref_kernel, grid_for(n), dim3(256), 0, s, (const float*)src,
+                       (uint16_t*)dst, n);
+    return hipGetLastError();
+  }
+  FL_DISPATCH(sdt, S, FL_DISPATCH(ddt, D, hipLaunchKernelGGL((cast_kernel<S, D>), grid_for(n),
+                                                             dim3(256), 0, s, (const S*)src,
+                                                             (D*)dst, n)));
+  return hipGetLastError();
+}
+
+hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(has_nan_kernel<T>, grid_for(n), dim3(256), 0, s,
+                                           (const T*)t, n, flag));
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(int dtype, const void* table, int cols, const int* idx, int n,
+                         void* out, hipStream_t s) {
+  const int64_t total = (int64_t)n * cols;
+  if (total <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(gather_kernel<T>, grid_for(total), dim3(256), 0, s,
+                                           (const T*)table, cols, idx, n, (T*)out));
+  return hipGetLastError();
+}
+
+hipError_t launch_slice(int dtype, const void* src, int cols, int r0, int r1, int c0, int c1,
+                        void* dst, hipStream_t s) {
+  const int ro = r1 - r0, co = c1 - c0;
+  const int64_t total = (int64_t)ro * co;
+  if (total <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(slice_kernel<T>, grid_for(total), dim3(256), 0, s,
+                                           (const T*)src, cols, r0, c0, ro, co, (T*)dst));
+  return hipGetLastError();
+}
+
+hipError_t launch_rope(int dtype, void* t, int rows, int heads, int head_dim, int ld,
+                       const int* pos, const float2* cs, hipStream_t s) {
+  const int64_t total = (int64_t)rows * heads * (head_dim / 2);
+  if (total <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(rope_kernel<T>, grid_for(total), dim3(256), 0, s,
+                                           (T*)t, rows, heads, head_dim, ld, pos, cs));
+  return hipGetLastError();
+}
+
+hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, const int* cu_seqlens,
+                                   int nseq, int max_len, int l2, float* partial, float* out,
+                                   int* nan_flag, int rows_per_chunk, hipStream_t s) {
+  if (nseq <= 0) return hipSuccess;
+  const int max_chunks = (max_len + rows_per_chunk - 1) / rows_per_chunk;
+  dim3 g1(max_chunks, nseq);
+  const int threads = cols >= 256 ? 256 : 64;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(pool_partial_kernel<T>, g1, dim3(threads), 0, s,
+                                           (const T*)hidden, cols, cu_seqlens, rows_per_chunk,
+                                           max_chunks, partial));
+  hipLaunchKernelGGL(pool_final_kernel, dim3(nseq), dim3(256), 0, s, partial, cols, cu_seqlens,
+                     rows_per_chunk, max_chunks, l2, out, nan_flag);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,
+                             int nseq, float* out, hipStream_t s) {
+  const int64_t total = (int64_t)nseq * cols;
+  if (total <= 0) return hipSuccess;
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(gather_cls_kernel<T>, grid_for(total), dim3(256), 0, s,
+                                           (const T*)hidden, cols, cu_seqlens, nseq, out));
+  return hipGetLastError();
+}
+
+}  // namespace fl

@@ -1,0 +1,450 @@
+// gemm.hip -- MFMA GEMMs for gfx950 with fused epilogues.
+//
+// Backs Tensor.Mul / Linear / LinearActivation (cpu_backend.go:316-372,
+// 612-660) and the encoder's projections (bert.go:610-824).  Layout:
+// activations A[M, K] row-major (tokens x features), weights B[N, K]
+// row-major (output features x input features, i.e. the reference's [in,out]
+// matrix packed transposed at load time).
+//
+// The weight tile is the MFMA "A" operand and the token tile the "B"
+// operand, so each lane of a 16x16 accumulator holds 4 consecutive output
+// features of one token: stores are 8/16-byte vectors and the RoPE pair
+// (j, j+32) and the SwiGLU (gate, up) pair land in the same lane.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+template <typename T> struct Mfma;
+template <> struct Mfma<_Float16> {
+  static constexpr int EPC = 8;  // elements per 16-byte fragment
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                               __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<__bf16> {
+  static constexpr int EPC = 8;
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<float> {
+  static constexpr int EPC = 4;
+  // Four k=4 steps; lane group g supplies k = 4g + j at step j for both
+  // operands, so the sum covers the 16 k values of the fragment.
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a[j]),
+                                               __builtin_bit_cast(float, b[j]), c, 0, 0, 0);
+  }
+};
+
+struct GemmParams {
+  const void* A;
+  const void* B;
+  void* C;
+  int lda, ldb, ldc;
+  int M, N, K;
+  GemmEpilogue epi;
+};
+
+template <typename T>
+__device__ inline void store4(T* dst, float4_t v) {
+  if constexpr (sizeof(T) == 4) {
+    *(float4_t*)dst = v;
+  } else if constexpr (Elem<T>::dtype == F16) {
+    half4_t h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *(half4_t*)dst = h;
+  } else {
+    bf16x4_t h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    *(bf16x4_t*)dst = h;
+  }
+}
+
+template <int EPI, int MATH>
+__device__ inline float4_t act4(float4_t v) {
+  if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = gelu_m<MATH>(v[i]);
+  } else if constexpr (EPI == EPI_TANH) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = tanh_m<MATH>(v[i]);
+  }
+  return v;
+}
+
+// BM x BN output tile per workgroup of WM x WN waves, K streamed in BK
+// slices through double-buffered LDS (rows padded by one 16-byte fragment so
+// the 16 lanes reading one fragment column hit distinct banks).
+template <typename T, int BM, int BN, int BK, int WM, int WN, int EPI, int MATH>
+__global__ void __launch_bounds__(WM* WN * 64) gemm_nt_kernel(GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int EPC = Mfma<T>::EPC;
+  constexpr int LS = BK + EPC;  // LDS row stride (elements)
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, FN = WTN / 16;
+  constexpr int CPR = BK / EPC;
+  constexpr int A_PER = BM * CPR / NT, B_PER = BN * CPR / NT;
+  constexpr int KSTEP = 4 * EPC;
+  static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "tile/thread mismatch");
+  static_assert(BK % KSTEP == 0 && WTM % 16 == 0 && WTN % 16 == 0, "bad tile");
+  static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SwiGLU needs gate/up tile pairs");
+  static_assert(EPI != EPI_ROPE || WTN % 64 == 0, "RoPE needs whole 64-wide heads per wave");
+
+  __shared__ __attribute__((aligned(16))) T smem[2 * (BM + BN) * LS];
+  T* As = smem;
+  T* Bs = smem + 2 * BM * LS;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Tile order: XCD-contiguous, then groups of 8 row-tiles sweeping all
+  // column tiles so concurrently resident tiles share A and B in L2.
+  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
+  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * num_n;
+  const int g = L / per_group;
+  const int first_m = g * GROUP_M;
+  const int gsize = min(num_m - first_m, GROUP_M);
+  const int r = L - g * per_group;
+  const int m0 = (first_m + r % gsize) * BM;
+  const int n0 = (r / gsize) * BN;
+
+  const T* A = (const T*)p.A;
+  const T* B = (const T*)p.B;
+  const int M = p.M;
+
+  u32x4_t ra[A_PER], rb[B_PER];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int c = tid + i * NT, row = c / CPR, col = (c % CPR) * EPC;
+      const int gm = m0 + row;
+      if (gm < M) ra[i] = *(const u32x4_t*)(A + (size_t)gm * p.lda + k0 + col);
+      else ra[i] = u32x4_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int c = tid + i * NT, row = c / CPR, col = (c % CPR) * EPC;
+      rb[i] = *(const u32x4_t*)(B + (size_t)(n0 + row) * p.ldb + k0 + col);
+    }
+  };
+  auto lstore = [&](int buf) {
+    T* as = As + buf * BM * LS;
+    T* bs = Bs + buf * BN * LS;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int c = tid + i * NT, row = c / CPR, col = (c % CPR) * EPC;
+      *(u32x4_t*)(as + row * LS + col) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int c = tid + i * NT, row = c / CPR, col = (c % CPR) * EPC;
+      *(u32x4_t*)(bs + row * LS + col) = rb[i];
+    }
+  };
+
+  float4_t acc[FN][TM];
+#pragma unroll
+  for (int f = 0; f < FN; ++f)
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[f][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = p.K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+    const T* as = As + cur * BM * LS + (wm * WTM + (lane & 15)) * LS;
+    const T* bs = Bs + cur * BN * LS + (wn * WTN + (lane & 15)) * LS;
+#pragma unroll
+    for (int ks = 0; ks < BK / KSTEP; ++ks) {
+      const int col = ks * KSTEP + (lane >> 4) * EPC;
+      u32x4_t fa[TM], fb[FN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) fa[t] = *(const u32x4_t*)(as + t * 16 * LS + col);
+#pragma unroll
+      for (int f = 0; f < FN; ++f) fb[f] = *(const u32x4_t*)(bs + f * 16 * LS + col);
+#pragma unroll
+      for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int t = 0; t < TM; ++t) Mfma<T>::mma(acc[f][t], fb[f], fa[t]);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  T* C = (T*)p.C;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int nbase = n0 + wn * WTN;
+  const float* bias = p.epi.bias;
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int m = m0 + wm * WTM + t * 16 + lrow;
+    if (m >= M) continue;
+    T* crow = C + (size_t)m * p.ldc;
+    if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int j = 0; j < FN / 2; ++j) {
+        const int ng = nbase + 2 * j * 16 + lgrp * 4;
+        float4_t gt = acc[2 * j][t], up = acc[2 * j + 1][t];
+        if (bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            gt[i] += bias[ng + i];
+            up[i] += bias[ng + 16 + i];
+          }
+        }
+        float4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = silu_m<MATH>(gt[i]) * up[i];
+        store4<T>(crow + nbase / 2 + j * 16 + lgrp * 4, o);
+      }
+    } else if constexpr (EPI == EPI_ROPE) {
+      const int ps = p.epi.pos[m];
+      const float2* cs = p.epi.rope_cs + (size_t)ps * 32;
+#pragma unroll
+      for (int h = 0; h < FN / 4; ++h) {
+        const int hb = nbase + h * 64;
+        float4_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = acc[h * 4 + q][t];
+          if (bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[q][i] += bias[hb + q * 16 + lgrp * 4 + i];
+          }
+        }
+        if (hb < p.epi.rope_cols) {
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float2 c = cs[q * 16 + lgrp * 4 + i];
+              const float x1 = v[q][i], x2 = v[q + 2][i];
+              v[q][i] = x1 * c.x - x2 * c.y;
+              v[q + 2][i] = x1 * c.y + x2 * c.x;
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) store4<T>(crow + hb + q * 16 + lgrp * 4, v[q]);
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < FN; ++f) {
+        const int n = nbase + f * 16 + lgrp * 4;
+        float4_t v = acc[f][t];
+        if (bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += bias[n + i];
+        }
+        store4<T>(crow + n, act4<EPI, MATH>(v));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile configurations
+// ---------------------------------------------------------------------------
+template <typename T> struct TileCfg;
+template <> struct TileCfg<_Float16> {
+  static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2;
+};
+template <> struct TileCfg<__bf16> {
+  static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2;
+};
+template <> struct TileCfg<float> {
+  static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1;
+};
+
+template <typename T, int EPI, int MATH>
+static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
+  using C = TileCfg<T>;
+  const int num_m = (p.M + C::BM - 1) / C::BM;
+  const int num_n = p.N / C::BN;
+  dim3 grid(num_m * num_n), block(C::WM * C::WN * 64);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, C::BM, C::BN, C::BK, C::WM, C::WN, EPI, MATH>), grid,
+                     block, 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
+  const bool ref = p.epi.math == MATH_REFERENCE;
+  switch (p.epi.kind) {
+    case EPI_STORE: return launch_cfg<T, EPI_STORE, MATH_EXACT>(p, s);
+    case EPI_ROPE: return launch_cfg<T, EPI_ROPE, MATH_EXACT>(p, s);
+    case EPI_GELU:
+      return ref ? launch_cfg<T, EPI_GELU, MATH_REFERENCE>(p, s)
+                 : launch_cfg<T, EPI_GELU, MATH_EXACT>(p, s);
+    case EPI_TANH:
+      return ref ? launch_cfg<T, EPI_TANH, MATH_REFERENCE>(p, s)
+                 : launch_cfg<T, EPI_TANH, MATH_EXACT>(p, s);
+    case EPI_SWIGLU:
+      return ref ? launch_cfg<T, EPI_SWIGLU, MATH_REFERENCE>(p, s)
+                 : launch_cfg<T, EPI_SWIGLU, MATH_EXACT>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+static bool cfg_ok(int N, int K) {
+  using C = TileCfg<T>;
+  return N % C::BN == 0 && K % C::BK == 0;
+}
+
+bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
+                       int ldb, const void* C, int ldc, const GemmEpilogue& epi) {
+  if (M <= 0 || N <= 0 || K <= 0) return false;
+  const int esz = dtype == F32 ? 4 : 2;
+  const int epc = 16 / esz;
+  bool shape = dtype == F32 ? cfg_ok<float>(N, K)
+                            : (dtype == F16 ? cfg_ok<_Float16>(N, K) : cfg_ok<__bf16>(N, K));
+  if (!shape) return false;
+  if (lda % epc || ldb % epc || ldc % 4) return false;
+  if (((uintptr_t)A | (uintptr_t)B) & 15) return false;
+  if ((uintptr_t)C & (4 * esz - 1)) return false;
+  if (epi.kind == EPI_SWIGLU && (N % 32)) return false;
+  if (epi.kind == EPI_ROPE && (epi.rope_cols % 64 || !epi.pos || !epi.rope_cs)) return false;
+  return true;
+}
+
+hipError_t launch_gemm_nt(int dtype, const void* A, int lda, const void* B, int ldb, void* C,
+                          int ldc, int M, int N, int K, const GemmEpilogue& epi,
+                          hipStream_t stream) {
+  GemmParams p{A, B, C, lda, ldb, ldc, M, N, K, epi};
+  switch (dtype) {
+    case F16: return launch_typed<_Float16>(p, stream);
+    case BF16: return launch_typed<__bf16>(p, stream);
+    case F32: return launch_typed<float>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Generic GEMM (any shape, transposes, alpha): 16x16 LDS tiles on the VALU.
+// Used for odd shapes of the per-op API; fp32 accumulation.
+// ---------------------------------------------------------------------------
+template <typename T, int MATH>
+__global__ void __launch_bounds__(256)
+gemm_generic_kernel(int ta, int tb, int M, int N, int K, float alpha, const T* A, int lda,
+                    const T* B, int ldb, T* C, int ldc, const float* bias, int act) {
+  __shared__ float sa[16][17], sb[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
+  float acc = 0.f;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    {
+      const int ar = blockIdx.y * 16 + ty, ak = k0 + tx;
+      float v = 0.f;
+      if (ar < M && ak < K) v = to_f(ta ? A[(size_t)ak * lda + ar] : A[(size_t)ar * lda + ak]);
+      sa[ty][tx] = v;
+      const int bk = k0 + ty, bc = blockIdx.x * 16 + tx;
+      float w = 0.f;
+      if (bk < K && bc < N) w = to_f(tb ? B[(size_t)bc * ldb + bk] : B[(size_t)bk * ldb + bc]);
+      sb[ty][tx] = w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) acc += sa[ty][kk] * sb[kk][tx];
+    __syncthreads();
+  }
+  if (row < M && col < N) {
+    float v = alpha * acc;
+    if (bias) v += bias[col];
+    if (act == ACT_GELU) v = gelu_m<MATH>(v);
+    else if (act == ACT_TANH) v = tanh_m<MATH>(v);
+    C[(size_t)row * ldc + col] = from_f<T>(v);
+  }
+}
+
+template <typename T>
+static hipError_t gen_typed(int ta, int tb, int M, int N, int K, float alpha, const void* A,
+                            int lda, const void* B, int ldb, void* C, int ldc, const float* bias,
+                            int act, int math, hipStream_t s) {
+  dim3 grid((N + 15) / 16, (M + 15) / 16), block(256);
+  if (math == MATH_REFERENCE)
+    hipLaunchKernelGGL((gemm_generic_kernel<T, MATH_REFERENCE>), grid, block, 0, s, ta, tb, M,
+                       N, K, alpha, (const T*)A, lda, (const T*)B, ldb, (T*)C, ldc, bias, act);
+  else
+    hipLaunchKernelGGL((gemm_generic_kernel<T, MATH_EXACT>), grid, block, 0, s, ta, tb, M, N, K,
+                       alpha, (const T*)A, lda, (const T*)B, ldb, (T*)C, ldc, bias, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N, int K,
+                               float alpha, const void* A, int lda, const void* B, int ldb,
+                               void* C, int ldc, const float* bias, int act, int math,
+                               hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  switch (dtype) {
+    case F32:
+      return gen_typed<float>(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, C, ldc, bias,
+                              act, math, s);
+    case F16:
+      return gen_typed<_Float16>(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, C, ldc, bias,
+                                 act, math, s);
+    case BF16:
+      return gen_typed<__bf16>(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, C, ldc, bias,
+                               act, math, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Weight packing: out[n][k] = in[k][n]; with SwiGLU interleave the [gate|up]
+// output columns are reordered into 16-column blocks g0 u0 g1 u1 ...
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int swiglu) {
+  __shared__ T tile[32][33];
+  const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int j = ty; j < 32; j += 8) {
+    const int r = by + j, c = bx + tx;
+    if (r < rows && c < cols) tile[j][tx] = in[(size_t)r * cols + c];
+  }
+  __syncthreads();
+  const int half = cols / 2;
+  for (int j = ty; j < 32; j += 8) {
+    const int n = bx + j, k = by + tx;  // output row n (input column), column k
+    if (n < cols && k < rows) {
+      int pn = n;
+      if (swiglu) pn = n < half ? (n / 16) * 32 + (n % 16) : ((n - half) / 16) * 32 + 16 + (n - half) % 16;
+      out[(size_t)pn * rows + k] = tile[tx][j];
+    }
+  }
+}
+
+hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
+                            int swiglu_interleave, hipStream_t s) {
+  dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(256);
+  switch (dtype) {
+    case F32:
+      hipLaunchKernelGGL(transpose_kernel<float>, grid, block, 0, s, (const float*)in, rows, cols,
+                         (float*)out, swiglu_interleave);
+      break;
+    case F16:
+      hipLaunchKernelGGL(transpose_kernel<_Float16>, grid, block, 0, s, (const _Float16*)in,
+                         rows, cols, (_Float16*)out, swiglu_interleave);
+      break;
+    case BF16:
+      hipLaunchKernelGGL(transpose_kernel<__bf16>, grid, block, 0, s, (const __bf16*)in, rows,
+                         cols, (__bf16*)out, swiglu_interleave);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fl

@@ -1,0 +1,112 @@
+// kernels.hpp -- host-side launchers of the gfx950 kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fl {
+
+enum EpiKind : int {
+  EPI_STORE = 0,   // out = acc + bias
+  EPI_GELU = 1,    // out = gelu(acc + bias)
+  EPI_TANH = 2,    // out = tanh(acc + bias)
+  EPI_SWIGLU = 3,  // gate/up interleaved in 16-column blocks -> out = silu(g) * u
+  EPI_ROPE = 4,    // rotate-half RoPE on columns [0, rope_cols), head_dim 64
+};
+
+struct GemmEpilogue {
+  int kind = EPI_STORE;
+  int math = 0;                    // MathMode for GELU / tanh / silu
+  const float* bias = nullptr;     // fp32 [N] (packed order) or null
+  const float2* rope_cs = nullptr; // [max_pos][32] (cos, sin)
+  const int* pos = nullptr;        // [M] position of each row in its sequence
+  int rope_cols = 0;
+};
+
+// C[M, N] = A[M, K] * B[N, K]^T with the epilogue.  MFMA path; requires
+// N % 64 == 0, K % 64 (16-bit) or K % 32 (fp32) == 0 and 16-byte aligned rows.
+bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
+                       int ldb, const void* C, int ldc, const GemmEpilogue& epi);
+hipError_t launch_gemm_nt(int dtype, const void* A, int lda, const void* B, int ldb, void* C,
+                          int ldc, int M, int N, int K, const GemmEpilogue& epi,
+                          hipStream_t stream);
+
+// Any shape / transpose: C = alpha * op(A) op(B) (+ bias, activation).
+hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N, int K,
+                               float alpha, const void* A, int lda, const void* B, int ldb,
+                               void* C, int ldc, const float* bias, int act, int math,
+                               hipStream_t stream);
+
+// out[n, k] = in[k, n] (dtype elements), optionally interleaving SwiGLU
+// gate/up halves in 16-row blocks.
+hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
+                            int swiglu_interleave, hipStream_t stream);
+
+// ---- attention ------------------------------------------------------------
+struct AttnWork {
+  int seq;     // sequence index
+  int head;    // head index
+  int q0;      // first query row (relative to the sequence start)
+  int pad;
+};
+// Flash attention (exact math, online softmax) for head_dim 64, 16-bit types.
+hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
+                                  int ldqkv, void* out, int ldo, const int* cu_seqlens,
+                                  const AttnWork* work, int n_work, float scale, int waves,
+                                  hipStream_t stream);
+// Two-pass attention (exact row max, then reference ExpFast or exp) for
+// head_dim 64 fp32.
+hipError_t launch_attention_f32(const float* q, const float* k, const float* v, int ldqkv,
+                                float* out, int ldo, const int* cu_seqlens,
+                                const AttnWork* work, int n_work, float scale, int math,
+                                hipStream_t stream);
+// Any head_dim / dtype: one thread per query row.
+hipError_t launch_attention_generic(int dtype, const void* q, const void* k, const void* v,
+                                    int ldqkv, void* out, int ldo, const int* cu_seqlens,
+                                    int nseq, int max_len, int heads, int head_dim, float scale,
+                                    int math, hipStream_t stream);
+
+// ---- normalisation / embedding ---------------------------------------------
+// t = LN(t [+ residual]) row-wise, fp32 statistics; gamma/beta fp32.
+hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
+                            const float* gamma, const float* beta, float eps,
+                            hipStream_t stream);
+// x[t] = LN(word[ids[t]] + pos[pos_ids[t]] (if pos) + type[0]).  Ids outside
+// [0, vocab) read row 0 and set *bad_id (never an out-of-bounds read).
+hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,
+                           const void* pos_table, const void* type_table, int T, int H,
+                           const float* gamma, const float* beta, float eps, int vocab,
+                           int* bad_id, void* out, hipStream_t stream);
+
+// ---- elementwise ------------------------------------------------------------
+hipError_t launch_add(int dtype, void* t, const void* o, int64_t n, hipStream_t s);
+hipError_t launch_affine(int dtype, void* t, int64_t n, float mul, float add, hipStream_t s);
+hipError_t launch_add_bias(int dtype, void* t, int rows, int cols, const void* bias,
+                           hipStream_t s);
+hipError_t launch_activation(int dtype, void* t, int rows, int cols, int act, int math,
+                             hipStream_t s);
+hipError_t launch_cast(const void* src, int sdt, void* dst, int ddt, int64_t n, int truncate_ref,
+                       hipStream_t s);
+hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStream_t s);
+hipError_t launch_gather(int dtype, const void* table, int cols, const int* idx, int n,
+                         void* out, hipStream_t s);
+hipError_t launch_slice(int dtype, const void* src, int cols, int r0, int r1, int c0, int c1,
+                        void* dst, hipStream_t s);
+// RoPE in place with positions pos[row] and a (cos, sin) table [max_pos][head_dim/2].
+hipError_t launch_rope(int dtype, void* t, int rows, int heads, int head_dim, int ld,
+                       const int* pos, const float2* cs, hipStream_t s);
+// Masked mean-pool (+L2) over cu_seqlens into fp32 out [nseq x cols]; sets
+// *nan_flag (if non-null) when any pooled value is NaN/Inf.  `partial` is
+// scratch of nseq * ceil(max_len / rows_per_chunk) * cols floats.
+hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, const int* cu_seqlens,
+                                   int nseq, int max_len, int l2, float* partial, float* out,
+                                   int* nan_flag, int rows_per_chunk, hipStream_t s);
+// out[r, c] = silu(in[r, c]) * in[r, inter + c] over an unfused [rows, 2*inter] product.
+hipError_t launch_swiglu(int dtype, const void* in, int rows, int inter, void* out, int math,
+                         hipStream_t s);
+// Gathers the first row of each sequence as fp32 [nseq x cols].
+hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,
+                             int nseq, float* out, hipStream_t s);
+
+}  // namespace fl

@@ -1,0 +1,734 @@
+// model.cpp -- model-level encoder forward (BertModel.ForwardBatch,
+// internal/embeddings/model/bert.go:149-169) on gfx950.
+//
+// Per layer (bert.go:364-384, 610-824):
+//   QKV   = X Wqkv^T + b        one GEMM, N = 3H, RoPE fused in the epilogue
+//   CTX   = attention(Q, K, V)  flash (16-bit) / two-pass (fp32), varlen
+//   TMP   = CTX Wo^T + bo
+//   X     = LN(X + TMP)         residual.AddLayerNorm (cpu_backend.go:603-610)
+//   G     = act(X Wi^T + bi)    GELU or SwiGLU fused in the epilogue
+//   TMP   = G Wd^T + bd
+//   X     = LN(X + TMP)
+// then masked mean-pool (+L2) or the CLS tanh pooler.
+//
+// Weights arrive in the reference layout ([in, out], Y = X W) and are packed
+// once: transposed to [out, in] so both GEMM operands stream along K,
+// Q|K|V concatenated, SwiGLU gate/up interleaved in 16-column blocks.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "context.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+struct LayerW {
+  void* wqkv = nullptr;  // [3H, H]
+  float* bqkv = nullptr; // [3H]
+  void* wo = nullptr;    // [H, H]
+  float* bo = nullptr;
+  float* ln1_g = nullptr;
+  float* ln1_b = nullptr;
+  void* wi = nullptr;    // [Ni, H] (SwiGLU interleaved)
+  float* bi = nullptr;   // [Ni] (same order)
+  void* wd = nullptr;    // [H, I]
+  float* bd = nullptr;
+  float* ln2_g = nullptr;
+  float* ln2_b = nullptr;
+};
+
+enum ProfClass { P_EMBED = 0, P_QKV, P_ATTN, P_O, P_LN, P_UP, P_DOWN, P_POOL };
+
+}  // namespace fl
+
+using namespace fl;
+
+struct fl_model {
+  fl_context* ctx = nullptr;
+  fl_model_config cfg{};
+  int H = 0, I = 0, Ni = 0, heads = 0, hd = 0, dtype = 0;
+  size_t esz = 2;
+  bool swiglu = false, rope = false;
+  bool mfma_qkv = false, mfma_o = false, mfma_up = false, mfma_down = false;
+  bool rope_fused = false;
+
+  void* word = nullptr;
+  void* pos = nullptr;
+  void* type = nullptr;
+  float* emb_g = nullptr;
+  float* emb_b = nullptr;
+  std::vector<LayerW> layers;
+  float* pool_w = nullptr;  // fp32 [H, H] reference layout
+  float* pool_b = nullptr;
+  std::vector<void*> owned;
+
+  // activations (capacity in tokens / sequences)
+  int64_t cap_tokens = 0;
+  int cap_seq = 0;
+  size_t cap_work = 0;
+  size_t cap_part = 0;
+  void* X = nullptr;
+  void* QKV = nullptr;  // also holds the FFN intermediate
+  void* CTX = nullptr;
+  void* TMP = nullptr;
+  void* G2 = nullptr;   // [T, 2I] unfused SwiGLU product (only without the fused epilogue)
+  int* ids32 = nullptr;
+  int* pos32 = nullptr;
+  int* cu = nullptr;
+  AttnWork* work = nullptr;
+  float* part = nullptr;
+  float* cls = nullptr;
+  float* out = nullptr;
+  int* flags = nullptr;  // [0] NaN in pooled output, [1] id out of range
+
+  std::vector<int64_t> last_lengths;
+  int64_t T = 0;
+  int n_work = 0, max_len = 0, waves = 4;
+  const float2* rope_cs = nullptr;
+
+  bool prof = false;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_next = 0;
+  std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
+  double prof_ms[FL_PROF_CLASSES] = {0};
+  int64_t prof_cnt[FL_PROF_CLASSES] = {0};
+};
+
+namespace {
+
+int track_alloc(fl_model* m, size_t bytes, void** out) {
+  int st = device_alloc(m->ctx, bytes, out);
+  if (st) return st;
+  m->owned.push_back(*out);
+  return FL_OK;
+}
+
+void untrack_free(fl_model* m, void* p) {
+  if (!p) return;
+  auto it = std::find(m->owned.begin(), m->owned.end(), p);
+  if (it != m->owned.end()) m->owned.erase(it);
+  (void)hipFree(p);
+}
+
+#define M_CHECK(expr)                                  \
+  do {                                                 \
+    hipError_t _e = (expr);                            \
+    if (_e != hipSuccess) return hip_fail(_e, #expr);  \
+  } while (0)
+
+#define M_ST(expr)        \
+  do {                    \
+    int _s = (expr);      \
+    if (_s) return _s;    \
+  } while (0)
+
+hipEvent_t next_event(fl_model* m) {
+  if (m->ev_next == m->ev_pool.size()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    m->ev_pool.push_back(e);
+  }
+  return m->ev_pool[m->ev_next++];
+}
+
+struct ProfScope {
+  fl_model* m;
+  int cls;
+  hipEvent_t a = nullptr;
+  ProfScope(fl_model* mm, int c) : m(mm), cls(c) {
+    if (m->prof) {
+      a = next_event(m);
+      if (a) (void)hipEventRecord(a, m->ctx->stream);
+    }
+  }
+  ~ProfScope() {
+    if (m->prof && a) {
+      hipEvent_t b = next_event(m);
+      if (b) {
+        (void)hipEventRecord(b, m->ctx->stream);
+        m->pending.push_back({cls, {a, b}});
+      }
+    }
+  }
+};
+
+int collect_profile(fl_model* m) {
+  if (m->pending.empty()) return FL_OK;
+  M_CHECK(hipStreamSynchronize(m->ctx->stream));
+  for (auto& p : m->pending) {
+    float ms = 0.f;
+    M_CHECK(hipEventElapsedTime(&ms, p.second.first, p.second.second));
+    m->prof_ms[p.first] += ms;
+    m->prof_cnt[p.first] += 1;
+  }
+  m->pending.clear();
+  m->ev_next = 0;
+  return FL_OK;
+}
+
+bool mfma_shape_ok(int dtype, int N, int K) {
+  GemmEpilogue e;
+  // Alignment of model-owned buffers is guaranteed; check the shape only.
+  static const char dummy[64] __attribute__((aligned(256))) = {0};
+  return gemm_nt_supported(dtype, 1, N, K, dummy, K, dummy, K, dummy, N, e);
+}
+
+int ensure_capacity(fl_model* m, int64_t T, int nseq, size_t nwork, size_t part_elems) {
+  if (T > m->cap_tokens) {
+    M_CHECK(hipStreamSynchronize(m->ctx->stream));
+    for (void* p : {m->X, m->QKV, m->CTX, m->TMP, m->G2, (void*)m->ids32, (void*)m->pos32})
+      untrack_free(m, p);
+    m->G2 = nullptr;
+    int64_t cap = std::max<int64_t>(T, 256);
+    const int64_t wide = std::max<int64_t>(3 * m->H, m->Ni);
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->X));
+    M_ST(track_alloc(m, (size_t)cap * wide * m->esz, &m->QKV));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->CTX));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->TMP));
+    if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, &m->G2));
+    void* p;
+    M_ST(track_alloc(m, (size_t)cap * 4, &p));
+    m->ids32 = (int*)p;
+    M_ST(track_alloc(m, (size_t)cap * 4, &p));
+    m->pos32 = (int*)p;
+    m->cap_tokens = cap;
+    m->last_lengths.clear();
+  }
+  if (nseq > m->cap_seq) {
+    M_CHECK(hipStreamSynchronize(m->ctx->stream));
+    for (void* p : {(void*)m->cu, (void*)m->cls, (void*)m->out}) untrack_free(m, p);
+    const int cap = std::max(nseq, 64);
+    void* p;
+    M_ST(track_alloc(m, (size_t)(cap + 1) * 4, &p));
+    m->cu = (int*)p;
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, &p));
+    m->cls = (float*)p;
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, &p));
+    m->out = (float*)p;
+    m->cap_seq = cap;
+    m->last_lengths.clear();
+  }
+  if (nwork > m->cap_work) {
+    M_CHECK(hipStreamSynchronize(m->ctx->stream));
+    untrack_free(m, m->work);
+    void* p;
+    M_ST(track_alloc(m, nwork * sizeof(AttnWork), &p));
+    m->work = (AttnWork*)p;
+    m->cap_work = nwork;
+    m->last_lengths.clear();
+  }
+  if (part_elems > m->cap_part) {
+    M_CHECK(hipStreamSynchronize(m->ctx->stream));
+    untrack_free(m, m->part);
+    void* p;
+    M_ST(track_alloc(m, part_elems * 4, &p));
+    m->part = (float*)p;
+    m->cap_part = part_elems;
+  }
+  return FL_OK;
+}
+
+constexpr int kPoolRows = 64;
+
+// Uploads cu_seqlens, per-token positions and the attention work list when
+// the batch's lengths differ from the previous call.
+int prepare(fl_model* m, const int64_t* lengths, int nseq) {
+  int64_t T = 0;
+  int max_len = 0;
+  for (int b = 0; b < nseq; ++b) {
+    if (lengths[b] <= 0) return fail(FL_ERR_INVALID, "sequence lengths must be positive");
+    T += lengths[b];
+    max_len = std::max<int>(max_len, (int)lengths[b]);
+  }
+  if (T >= (int64_t)1 << 31) return fail(FL_ERR_INVALID, "too many tokens");
+  const bool fast_attn = m->hd == 64;
+  const int waves = max_len > 64 ? 4 : 2;
+  const int bq = m->dtype == FL_F32 ? 64 : waves * 32;
+  size_t nwork = 0;
+  if (fast_attn)
+    for (int b = 0; b < nseq; ++b) nwork += (size_t)m->heads * ((lengths[b] + bq - 1) / bq);
+  const size_t part = (size_t)nseq * ((max_len + kPoolRows - 1) / kPoolRows) * m->H;
+  M_ST(ensure_capacity(m, T, nseq, std::max<size_t>(nwork, 1), part));
+
+  const bool same = (int)m->last_lengths.size() == nseq &&
+                    std::equal(m->last_lengths.begin(), m->last_lengths.end(), lengths);
+  if (!same) {
+    std::vector<int> cu(nseq + 1, 0), pos((size_t)T);
+    for (int b = 0; b < nseq; ++b) {
+      cu[b + 1] = cu[b] + (int)lengths[b];
+      for (int i = 0; i < (int)lengths[b]; ++i) {
+        // bert.go:223-234: absolute positions restart per sequence and clamp
+        // at MaxPositionEmbeddings-1; RoPE uses the in-sequence index.
+        pos[cu[b] + i] = m->rope ? i : std::min(i, m->cfg.max_pos - 1);
+      }
+    }
+    std::vector<AttnWork> work;
+    work.reserve(nwork);
+    if (fast_attn) {
+      std::vector<int> order(nseq);
+      for (int b = 0; b < nseq; ++b) order[b] = b;
+      std::stable_sort(order.begin(), order.end(),
+                       [&](int a, int b) { return lengths[a] > lengths[b]; });
+      for (int b : order)
+        for (int h = 0; h < m->heads; ++h)
+          for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work.push_back(AttnWork{b, h, q0, 0});
+    }
+    if (m->rope) {
+      int st;
+      m->rope_cs = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st);
+      if (st) return st;
+    }
+    hipStream_t s = m->ctx->stream;
+    M_CHECK(hipMemcpyAsync(m->cu, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, s));
+    M_CHECK(hipMemcpyAsync(m->pos32, pos.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
+    if (!work.empty())
+      M_CHECK(hipMemcpyAsync(m->work, work.data(), work.size() * sizeof(AttnWork),
+                             hipMemcpyHostToDevice, s));
+    M_CHECK(hipStreamSynchronize(s));
+    m->last_lengths.assign(lengths, lengths + nseq);
+    m->n_work = (int)work.size();
+    m->waves = waves;
+  }
+  m->T = T;
+  m->max_len = max_len;
+  return FL_OK;
+}
+
+int gemm(fl_model* m, bool mfma, const void* A, const void* W, void* C, int M, int N, int K,
+         const GemmEpilogue& epi) {
+  hipStream_t s = m->ctx->stream;
+  if (mfma) {
+    M_CHECK(launch_gemm_nt(m->dtype, A, K, W, K, C, epi.kind == EPI_SWIGLU ? N / 2 : N, M, N, K,
+                           epi, s));
+    return FL_OK;
+  }
+  int act = epi.kind == EPI_GELU ? FL_ACT_GELU : (epi.kind == EPI_TANH ? FL_ACT_TANH : FL_ACT_IDENTITY);
+  M_CHECK(launch_gemm_generic(m->dtype, 0, 1, M, N, K, 1.0f, A, K, W, K, C, N, epi.bias, act,
+                              epi.math, s));
+  return FL_OK;
+}
+
+// The forward on device-resident ids (m->ids32 or caller memory) into d_out.
+int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
+  hipStream_t s = m->ctx->stream;
+  const int64_t T = m->T;
+  const int H = m->H, dt = m->dtype;
+  const int Ti = (int)T;
+  M_CHECK(hipMemsetAsync(m->flags, 0, 8, s));
+  {
+    ProfScope ps(m, P_EMBED);
+    M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : m->pos32, m->word,
+                            m->rope ? nullptr : m->pos, m->type, Ti, H, m->emb_g, m->emb_b,
+                            m->cfg.ln_eps, m->cfg.vocab_size, m->flags + 1, m->X, s));
+  }
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const LayerW& w = m->layers[l];
+    {
+      ProfScope ps(m, P_QKV);
+      GemmEpilogue e;
+      e.bias = w.bqkv;
+      if (m->rope && m->rope_fused) {
+        e.kind = EPI_ROPE;
+        e.rope_cs = m->rope_cs;
+        e.pos = m->pos32;
+        e.rope_cols = 2 * H;
+      }
+      M_ST(gemm(m, m->mfma_qkv, m->X, w.wqkv, m->QKV, Ti, 3 * H, H, e));
+      if (m->rope && !m->rope_fused)
+        M_CHECK(launch_rope(dt, m->QKV, Ti, 2 * m->heads, m->hd, 3 * H, m->pos32, m->rope_cs, s));
+    }
+    {
+      ProfScope ps(m, P_ATTN);
+      const float scale = 1.0f / (float)std::sqrt((double)m->hd);  // bert.go:643
+      const char* q = (const char*)m->QKV;
+      const void* k = q + (size_t)H * m->esz;
+      const void* v = q + (size_t)2 * H * m->esz;
+      if (m->hd == 64 && dt != FL_F32)
+        M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, m->CTX, H, m->cu, m->work, m->n_work,
+                                       scale, m->waves, s));
+      else if (m->hd == 64)
+        M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
+                                     (float*)m->CTX, H, m->cu, m->work, m->n_work, scale,
+                                     m->cfg.math, s));
+      else
+        M_CHECK(launch_attention_generic(dt, q, k, v, 3 * H, m->CTX, H, m->cu, nseq, m->max_len,
+                                         m->heads, m->hd, scale, m->cfg.math, s));
+    }
+    {
+      ProfScope ps(m, P_O);
+      GemmEpilogue e;
+      e.bias = w.bo;
+      M_ST(gemm(m, m->mfma_o, m->CTX, w.wo, m->TMP, Ti, H, H, e));
+    }
+    {
+      ProfScope ps(m, P_LN);
+      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s));
+    }
+    {
+      ProfScope ps(m, P_UP);
+      GemmEpilogue e;
+      e.bias = w.bi;
+      e.math = m->cfg.math;
+      if (m->swiglu) {
+        if (m->mfma_up) {
+          e.kind = EPI_SWIGLU;
+          M_ST(gemm(m, true, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
+        } else {
+          // Unfused: [T, 2I] product, then silu(gate) * up into QKV.
+          M_ST(gemm(m, false, m->X, w.wi, m->G2, Ti, m->Ni, H, e));
+          M_CHECK(launch_swiglu(dt, m->G2, Ti, m->I, m->QKV, m->cfg.math, s));
+        }
+      } else {
+        e.kind = EPI_GELU;
+        M_ST(gemm(m, m->mfma_up, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
+      }
+    }
+    {
+      ProfScope ps(m, P_DOWN);
+      GemmEpilogue e;
+      e.bias = w.bd;
+      M_ST(gemm(m, m->mfma_down, m->QKV, w.wd, m->TMP, Ti, H, m->I, e));
+    }
+    {
+      ProfScope ps(m, P_LN);
+      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s));
+    }
+  }
+  {
+    ProfScope ps(m, P_POOL);
+    if (m->cfg.pool == FL_POOL_CLS_TANH) {
+      // BertPooler (bert.go:441-488) in fp32 (bert.go:459-476 forces fp32 for fp16 weights).
+      M_CHECK(launch_gather_cls(dt, m->X, H, m->cu, nseq, m->cls, s));
+      M_CHECK(launch_gemm_generic(FL_F32, 0, 0, nseq, H, H, 1.0f, m->cls, H, m->pool_w, H, d_out,
+                                  H, m->pool_b, FL_ACT_TANH, m->cfg.math, s));
+      M_CHECK(launch_has_nan(d_out, FL_F32, (int64_t)nseq * H, m->flags, s));
+    } else {
+      M_CHECK(launch_mean_pool_staged(dt, m->X, H, m->cu, nseq, m->max_len,
+                                      m->cfg.pool == FL_POOL_MEAN_L2, m->part, d_out, m->flags,
+                                      kPoolRows, s));
+    }
+  }
+  return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out) {
+  if (!ctx || !cfg || !out) return fail(FL_ERR_INVALID, "null argument");
+  std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+  M_ST(activate(ctx));
+  *out = nullptr;
+  const fl_model_config& c = *cfg;
+  if (c.hidden <= 0 || c.layers < 0 || c.heads <= 0 || c.hidden % c.heads || c.intermediate <= 0 ||
+      c.vocab_size <= 0 || c.max_pos <= 0)
+    return fail(FL_ERR_INVALID, "bad model shape");
+  if (c.activation != FL_ACT_GELU && c.activation != FL_ACT_SWIGLU)
+    return fail(FL_ERR_UNSUPPORTED, "intermediate activation must be GELU or SwiGLU");
+  if (c.position != FL_POS_ABSOLUTE && c.position != FL_POS_ROPE)
+    return fail(FL_ERR_INVALID, "bad position type");
+  if (c.dtype != FL_F32 && c.dtype != FL_F16 && c.dtype != FL_BF16)
+    return fail(FL_ERR_INVALID, "bad dtype");
+  if (c.pool < FL_POOL_CLS_TANH || c.pool > FL_POOL_MEAN_L2) return fail(FL_ERR_INVALID, "bad pool");
+  if ((c.hidden / c.heads) % 2 && c.position == FL_POS_ROPE)
+    return fail(FL_ERR_INVALID, "RoPE needs an even head size");
+  auto* m = new fl_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  m->H = c.hidden;
+  m->I = c.intermediate;
+  m->swiglu = c.activation == FL_ACT_SWIGLU;
+  m->Ni = m->swiglu ? 2 * m->I : m->I;
+  m->heads = c.heads;
+  m->hd = c.hidden / c.heads;
+  m->dtype = c.dtype;
+  m->esz = dtype_size(c.dtype);
+  m->rope = c.position == FL_POS_ROPE;
+  m->mfma_qkv = mfma_shape_ok(m->dtype, 3 * m->H, m->H);
+  m->mfma_o = mfma_shape_ok(m->dtype, m->H, m->H);
+  m->mfma_up = mfma_shape_ok(m->dtype, m->Ni, m->H) && (!m->swiglu || m->I % 16 == 0);
+  m->mfma_down = mfma_shape_ok(m->dtype, m->H, m->I);
+  m->rope_fused = m->mfma_qkv && m->hd == 64;
+
+  auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
+    void* p;
+    M_ST(track_alloc(m, n * 4, &p));
+    std::vector<float> h(n, v);
+    M_CHECK(hipMemcpy(p, h.data(), n * 4, hipMemcpyHostToDevice));
+    *dst = (float*)p;
+    return FL_OK;
+  };
+  auto zeros = [&](void** dst, size_t bytes) -> int {
+    M_ST(track_alloc(m, bytes, dst));
+    M_CHECK(hipMemset(*dst, 0, bytes));
+    return FL_OK;
+  };
+  int st = FL_OK;
+  const size_t H = m->H, I = m->I, Ni = m->Ni;
+  do {
+    if ((st = zeros(&m->word, (size_t)c.vocab_size * H * m->esz))) break;
+    if (!m->rope && (st = zeros(&m->pos, (size_t)c.max_pos * H * m->esz))) break;
+    if ((st = zeros(&m->type, 2 * H * m->esz))) break;
+    // NewLayerNorm (bert.go:271-283): gamma = 1, beta = 0.
+    if ((st = fill_f32(&m->emb_g, H, 1.f)) || (st = fill_f32(&m->emb_b, H, 0.f))) break;
+    m->layers.resize(c.layers);
+    for (auto& L : m->layers) {
+      if ((st = zeros(&L.wqkv, 3 * H * H * m->esz)) || (st = fill_f32(&L.bqkv, 3 * H, 0.f)) ||
+          (st = zeros(&L.wo, H * H * m->esz)) || (st = fill_f32(&L.bo, H, 0.f)) ||
+          (st = fill_f32(&L.ln1_g, H, 1.f)) || (st = fill_f32(&L.ln1_b, H, 0.f)) ||
+          (st = zeros(&L.wi, Ni * H * m->esz)) || (st = fill_f32(&L.bi, Ni, 0.f)) ||
+          (st = zeros(&L.wd, H * I * m->esz)) || (st = fill_f32(&L.bd, H, 0.f)) ||
+          (st = fill_f32(&L.ln2_g, H, 1.f)) || (st = fill_f32(&L.ln2_b, H, 0.f)))
+        break;
+    }
+    if (st) break;
+    if ((st = fill_f32(&m->pool_w, H * H, 0.f)) || (st = fill_f32(&m->pool_b, H, 0.f))) break;
+    void* f;
+    if ((st = zeros(&f, 256))) break;
+    m->flags = (int*)f;
+  } while (0);
+  if (st) {
+    for (void* p : m->owned) (void)hipFree(p);
+    delete m;
+    return st;
+  }
+  *out = m;
+  return FL_OK;
+}
+
+int fl_model_free(fl_model* m) {
+  if (!m) return FL_OK;
+  {
+    std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+    (void)activate(m->ctx);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    for (void* p : m->owned) (void)hipFree(p);
+    for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
+  }
+  delete m;
+  return FL_OK;
+}
+
+int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_t n) {
+  if (!m || !name || (!data && n)) return fail(FL_ERR_INVALID, "null argument");
+  fl_context* ctx = m->ctx;
+  std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+  M_ST(activate(ctx));
+  std::string nm(name), field = nm;
+  int layer = -1;
+  const size_t dot = nm.find('.');
+  if (dot != std::string::npos) {
+    field = nm.substr(0, dot);
+    char* end = nullptr;
+    layer = (int)std::strtol(nm.c_str() + dot + 1, &end, 10);
+    if (!end || *end || layer < 0 || layer >= (int)m->layers.size())
+      return fail(FL_ERR_INVALID, "bad layer index in weight name: " + nm);
+  }
+  const int64_t H = m->H, I = m->I, Ni = m->Ni, V = m->cfg.vocab_size;
+  hipStream_t s = ctx->stream;
+  const int dt = m->dtype;
+  const bool per_layer = layer >= 0;
+  auto expect = [&](int64_t want) -> int {
+    if (n != want)
+      return fail(FL_ERR_INVALID, "weight " + nm + ": expected " + std::to_string(want) +
+                                      " values, got " + std::to_string(n));
+    return FL_OK;
+  };
+  // Host fp32 -> scratch: [fp32 copy][dtype copy]
+  int st;
+  char* ws = (char*)workspace(ctx, ((size_t)n * 4 + 255) / 256 * 256 + (size_t)n * 4, &st);
+  if (st) return st;
+  float* f32 = (float*)ws;
+  void* cvt = ws + ((size_t)n * 4 + 255) / 256 * 256;
+  M_CHECK(hipMemcpyAsync(f32, data, (size_t)n * 4, hipMemcpyHostToDevice, s));
+  auto to_dtype = [&](void* dst) -> int {
+    M_CHECK(launch_cast(f32, FL_F32, dst, dt, n, 0, s));
+    return FL_OK;
+  };
+  auto copy_f32 = [&](float* dst) -> int {
+    M_CHECK(hipMemcpyAsync(dst, f32, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+    return FL_OK;
+  };
+  // [in, out] reference matrix -> [out, in] packed (optionally SwiGLU interleaved)
+  auto pack = [&](void* dst, int rows, int cols, int inter) -> int {
+    M_CHECK(launch_cast(f32, FL_F32, cvt, dt, n, 0, s));
+    M_CHECK(launch_transpose(dt, cvt, rows, cols, dst, inter, s));
+    return FL_OK;
+  };
+  if (!per_layer) {
+    if (field == "word_emb") { M_ST(expect(V * H)); M_ST(to_dtype(m->word)); }
+    else if (field == "pos_emb") {
+      M_ST(expect((int64_t)m->cfg.max_pos * H));
+      if (m->pos) M_ST(to_dtype(m->pos));  // unused by RoPE models (bert.go:222)
+    }
+    else if (field == "type_emb") { M_ST(expect(2 * H)); M_ST(to_dtype(m->type)); }
+    else if (field == "emb_ln_g") { M_ST(expect(H)); M_ST(copy_f32(m->emb_g)); }
+    else if (field == "emb_ln_b") { M_ST(expect(H)); M_ST(copy_f32(m->emb_b)); }
+    else if (field == "pool_w") { M_ST(expect(H * H)); M_ST(copy_f32(m->pool_w)); }
+    else if (field == "pool_b") { M_ST(expect(H)); M_ST(copy_f32(m->pool_b)); }
+    else return fail(FL_ERR_INVALID, "unknown weight " + nm);
+  } else {
+    LayerW& L = m->layers[layer];
+    const size_t esz = m->esz;
+    if (field == "q_w" || field == "k_w" || field == "v_w") {
+      M_ST(expect(H * H));
+      const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
+      M_ST(pack((char*)L.wqkv + (size_t)part * H * H * esz, (int)H, (int)H, 0));
+    } else if (field == "q_b" || field == "k_b" || field == "v_b") {
+      M_ST(expect(H));
+      const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
+      M_ST(copy_f32(L.bqkv + part * H));
+    } else if (field == "o_w") { M_ST(expect(H * H)); M_ST(pack(L.wo, (int)H, (int)H, 0)); }
+    else if (field == "o_b") { M_ST(expect(H)); M_ST(copy_f32(L.bo)); }
+    else if (field == "attn_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_g)); }
+    else if (field == "attn_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_b)); }
+    else if (field == "inter_w") {
+      M_ST(expect(H * Ni));
+      M_ST(pack(L.wi, (int)H, (int)Ni, m->swiglu && m->mfma_up));
+    } else if (field == "inter_b") {
+      M_ST(expect(Ni));
+      if (m->swiglu && m->mfma_up) {
+        std::vector<float> perm(Ni);
+        for (int64_t j = 0; j < Ni; ++j) {
+          const int64_t p = j < I ? (j / 16) * 32 + j % 16 : ((j - I) / 16) * 32 + 16 + (j - I) % 16;
+          perm[p] = data[j];
+        }
+        M_CHECK(hipMemcpyAsync(L.bi, perm.data(), Ni * 4, hipMemcpyHostToDevice, s));
+        M_CHECK(hipStreamSynchronize(s));
+      } else {
+        M_ST(copy_f32(L.bi));
+      }
+    } else if (field == "out_w") { M_ST(expect(I * H)); M_ST(pack(L.wd, (int)I, (int)H, 0)); }
+    else if (field == "out_b") { M_ST(expect(H)); M_ST(copy_f32(L.bd)); }
+    else if (field == "out_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_g)); }
+    else if (field == "out_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_b)); }
+    else return fail(FL_ERR_INVALID, "unknown weight " + nm);
+  }
+  M_CHECK(hipStreamSynchronize(s));
+  return FL_OK;
+}
+
+static int forward_common(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
+                          float* out) {
+  if (nseq <= 0) return FL_OK;
+  M_ST(prepare(m, lengths, nseq));
+  const int64_t T = m->T;
+  std::vector<int> i32((size_t)T);
+  for (int64_t t = 0; t < T; ++t) {
+    // cpu_backend.go:500-502: out-of-range ids are an error.
+    if (ids[t] < 0 || ids[t] >= m->cfg.vocab_size)
+      return fail(FL_ERR_INVALID, "Gather index out of bounds");
+    i32[t] = (int)ids[t];
+  }
+  hipStream_t s = m->ctx->stream;
+  M_CHECK(hipMemcpyAsync(m->ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
+  M_ST(run(m, m->ids32, nseq, m->out));
+  M_CHECK(hipMemcpyAsync(out, m->out, (size_t)nseq * m->H * 4, hipMemcpyDeviceToHost, s));
+  M_CHECK(hipStreamSynchronize(s));
+  return FL_OK;
+}
+
+int fl_model_forward(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
+                     float* out) {
+  if (!m || (nseq > 0 && (!ids || !lengths || !out))) return fail(FL_ERR_INVALID, "null argument");
+  if (nseq < 0) return fail(FL_ERR_INVALID, "negative batch");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  return forward_common(m, ids, lengths, nseq, out);
+}
+
+int fl_model_forward_padded(fl_model* m, const int64_t* ids, const int64_t* mask, int nseq,
+                            int max_len, float* out) {
+  if (!m || (nseq > 0 && (!ids || !mask || !out))) return fail(FL_ERR_INVALID, "null argument");
+  if (nseq < 0 || max_len <= 0) return fail(FL_ERR_INVALID, "bad padded shape");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  std::vector<int64_t> packed, lengths(nseq);
+  packed.reserve((size_t)nseq * max_len);
+  for (int b = 0; b < nseq; ++b) {
+    int64_t L = 0;
+    bool ended = false;
+    for (int t = 0; t < max_len; ++t) {
+      const int64_t mk = mask[(size_t)b * max_len + t];
+      if (mk) {
+        if (ended) return fail(FL_ERR_UNSUPPORTED, "mask must be right padding (1...1 0...0)");
+        packed.push_back(ids[(size_t)b * max_len + t]);
+        ++L;
+      } else {
+        ended = true;
+      }
+    }
+    if (L == 0) return fail(FL_ERR_INVALID, "sequence with no tokens");
+    lengths[b] = L;
+  }
+  return forward_common(m, packed.data(), lengths.data(), nseq, out);
+}
+
+int fl_model_forward_device(fl_model* m, const int32_t* d_ids, const int64_t* lengths, int nseq,
+                            float* d_out) {
+  if (!m || (nseq > 0 && (!d_ids || !lengths || !d_out)))
+    return fail(FL_ERR_INVALID, "null argument");
+  if (nseq < 0) return fail(FL_ERR_INVALID, "negative batch");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  if (nseq == 0) return FL_OK;
+  M_ST(prepare(m, lengths, nseq));
+  return run(m, d_ids, nseq, d_out);
+}
+
+int fl_model_status(fl_model* m, int* nan_in_output, int* bad_ids) {
+  if (!m) return fail(FL_ERR_INVALID, "null model");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  int h[2] = {0, 0};
+  M_CHECK(hipMemcpyAsync(h, m->flags, 8, hipMemcpyDeviceToHost, m->ctx->stream));
+  M_CHECK(hipStreamSynchronize(m->ctx->stream));
+  if (nan_in_output) *nan_in_output = h[0] != 0;
+  if (bad_ids) *bad_ids = h[1] != 0;
+  return FL_OK;
+}
+
+int fl_model_last_hidden(fl_model* m, float* out, int64_t n) {
+  if (!m || !out) return fail(FL_ERR_INVALID, "null argument");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  if (n != m->T * m->H) return fail(FL_ERR_INVALID, "size mismatch");
+  int st;
+  void* tmp = workspace(m->ctx, (size_t)n * 4, &st);
+  if (st) return st;
+  M_CHECK(launch_cast(m->X, m->dtype, tmp, FL_F32, n, 0, m->ctx->stream));
+  M_CHECK(hipMemcpyAsync(out, tmp, (size_t)n * 4, hipMemcpyDeviceToHost, m->ctx->stream));
+  M_CHECK(hipStreamSynchronize(m->ctx->stream));
+  return FL_OK;
+}
+
+int fl_model_set_profiling(fl_model* m, int enabled) {
+  if (!m) return fail(FL_ERR_INVALID, "null model");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  M_ST(collect_profile(m));
+  m->prof = enabled != 0;
+  for (int i = 0; i < FL_PROF_CLASSES; ++i) {
+    m->prof_ms[i] = 0;
+    m->prof_cnt[i] = 0;
+  }
+  return FL_OK;
+}
+
+int fl_model_profile_read(fl_model* m, double* ms, int64_t* count) {
+  if (!m || !ms || !count) return fail(FL_ERR_INVALID, "null argument");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  M_ST(collect_profile(m));
+  for (int i = 0; i < FL_PROF_CLASSES; ++i) {
+    ms[i] = m->prof_ms[i];
+    count[i] = m->prof_cnt[i];
+  }
+  return FL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,258 @@
+// norm.hip -- LayerNorm, residual+LayerNorm and the fused embedding kernel.
+//
+// LayerNorm follows cpu_backend.go:541-601: mean = sum/cols, variance =
+// sum((x-mean)^2)/cols (two passes, here over registers), invStd =
+// 1/float32(sqrt(float64(var+eps))), y = (x-mean)*invStd*gamma + beta, with
+// fp32 statistics whatever the storage type.  AddLayerNorm
+// (cpu_backend.go:603-610) adds the residual first.  One wave per row: a
+// row of H = 768 is 12 values per lane held in registers, so every element is
+// read once and written once.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fl {
+
+// Loads VEC consecutive elements starting at p as floats.
+template <typename T, int VEC>
+__device__ inline void load_vec(const T* p, float* out) {
+  if constexpr (VEC == 4 && sizeof(T) == 2) {
+    using V4 = T __attribute__((ext_vector_type(4)));
+    V4 v = *(const V4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = to_f(v[i]);
+  } else if constexpr (VEC == 4 && sizeof(T) == 4) {
+    float4_t v = *(const float4_t*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = to_f(p[i]);
+  }
+}
+
+template <typename T, int VEC>
+__device__ inline void store_vec(T* p, const float* in) {
+  if constexpr (VEC == 4 && sizeof(T) == 2) {
+    using V4 = T __attribute__((ext_vector_type(4)));
+    V4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = from_f<T>(in[i]);
+    *(V4*)p = v;
+  } else if constexpr (VEC == 4 && sizeof(T) == 4) {
+    *(float4_t*)p = float4_t{in[0], in[1], in[2], in[3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) p[i] = from_f<T>(in[i]);
+  }
+}
+
+// Normalises x[NCH][VEC] (this lane's share of one row; `valid` masks the
+// tail) in place.
+template <int NCH, int VEC>
+__device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], int cols,
+                               const float* gamma, const float* beta, const int (&col0)[NCH],
+                               float eps) {
+#pragma clang fp contract(off)
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c])
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) s += x[c][i];
+  s = wave_sum(s);
+  const float mean = s / (float)cols;
+  float v = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c])
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float d = x[c][i] - mean;
+        v += d * d;
+      }
+  v = wave_sum(v);
+  const float var = v / (float)cols;
+  const float inv = 1.0f / (float)sqrt((double)(var + eps));
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c])
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        x[c][i] = (x[c][i] - mean) * inv * gamma[col0[c] + i] + beta[col0[c] + i];
+}
+
+template <typename T, int NCH, int VEC>
+__global__ void __launch_bounds__(256)
+layernorm_kernel(T* t, const T* residual, int rows, int cols, const float* gamma,
+                 const float* beta, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  T* tr = t + (size_t)row * cols;
+  const T* rr = residual ? residual + (size_t)row * cols : nullptr;
+  float x[NCH][VEC];
+  bool valid[NCH];
+  int col0[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    col0[c] = (lane + c * 64) * VEC;
+    valid[c] = col0[c] < cols;
+    if (valid[c]) {
+      load_vec<T, VEC>(tr + col0[c], x[c]);
+      if (rr) {
+        float r[VEC];
+        load_vec<T, VEC>(rr + col0[c], r);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + r[i];
+      }
+    }
+  }
+  ln_core<NCH, VEC>(x, valid, cols, gamma, beta, col0, eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c]) store_vec<T, VEC>(tr + col0[c], x[c]);
+}
+
+template <typename T, int NCH, int VEC>
+static hipError_t ln_launch(void* t, const void* res, int rows, int cols, const float* g,
+                            const float* b, float eps, hipStream_t s) {
+  hipLaunchKernelGGL((layernorm_kernel<T, NCH, VEC>), dim3((rows + 3) / 4), dim3(256), 0, s,
+                     (T*)t, (const T*)res, rows, cols, g, b, eps);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t ln_typed(void* t, const void* res, int rows, int cols, const float* g,
+                           const float* b, float eps, hipStream_t s) {
+  if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res) % (4 * sizeof(T)) == 0)) {
+    const int nch = (cols / 4 + 63) / 64;
+    if (nch <= 1) return ln_launch<T, 1, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 2) return ln_launch<T, 2, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 3) return ln_launch<T, 3, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 4) return ln_launch<T, 4, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 8) return ln_launch<T, 8, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 16) return ln_launch<T, 16, 4>(t, res, rows, cols, g, b, eps, s);
+    return hipErrorInvalidValue;
+  }
+  const int nch = (cols + 63) / 64;
+  if (nch <= 2) return ln_launch<T, 2, 1>(t, res, rows, cols, g, b, eps, s);
+  if (nch <= 8) return ln_launch<T, 8, 1>(t, res, rows, cols, g, b, eps, s);
+  if (nch <= 32) return ln_launch<T, 32, 1>(t, res, rows, cols, g, b, eps, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
+                            const float* gamma, const float* beta, float eps,
+                            hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  switch (dtype) {
+    case F32: return ln_typed<float>(t, residual, rows, cols, gamma, beta, eps, stream);
+    case F16: return ln_typed<_Float16>(t, residual, rows, cols, gamma, beta, eps, stream);
+    case BF16: return ln_typed<__bf16>(t, residual, rows, cols, gamma, beta, eps, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Fused embedding (BertEmbeddings.ForwardBatch, bert.go:215-261):
+// x = (word[id] + pos[p]) + type[0], then LayerNorm, one write.
+// ---------------------------------------------------------------------------
+template <typename T, int NCH, int VEC>
+__global__ void __launch_bounds__(256)
+embed_ln_kernel(const int* ids, const int* pos_ids, const T* word, const T* pos_table,
+                const T* type_table, int rows, int cols, const float* gamma, const float* beta,
+                float eps, int vocab, int* bad_id, T* out) {
+#pragma clang fp contract(off)
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  int id = ids[row];
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(bad_id, 1);
+    id = 0;
+  }
+  const T* wr = word + (size_t)id * cols;
+  const T* pr = pos_table ? pos_table + (size_t)pos_ids[row] * cols : nullptr;
+  float x[NCH][VEC];
+  bool valid[NCH];
+  int col0[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    col0[c] = (lane + c * 64) * VEC;
+    valid[c] = col0[c] < cols;
+    if (valid[c]) {
+      load_vec<T, VEC>(wr + col0[c], x[c]);
+      float y[VEC];
+      if (pr) {
+        load_vec<T, VEC>(pr + col0[c], y);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + y[i];
+      }
+      load_vec<T, VEC>(type_table + col0[c], y);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + y[i];
+    }
+  }
+  ln_core<NCH, VEC>(x, valid, cols, gamma, beta, col0, eps);
+  T* orow = out + (size_t)row * cols;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c]) store_vec<T, VEC>(orow + col0[c], x[c]);
+}
+
+struct EmbArgs {
+  const int* ids;
+  const int* pos_ids;
+  const void* word;
+  const void* pos_table;
+  const void* type_table;
+  int T, H;
+  const float* g;
+  const float* b;
+  float eps;
+  int vocab;
+  int* bad_id;
+  void* out;
+};
+
+template <typename T, int NCH, int VEC>
+static hipError_t emb_launch(const EmbArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((embed_ln_kernel<T, NCH, VEC>), dim3((a.T + 3) / 4), dim3(256), 0, s, a.ids,
+                     a.pos_ids, (const T*)a.word, (const T*)a.pos_table, (const T*)a.type_table,
+                     a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id, (T*)a.out);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t emb_typed(const EmbArgs& a, hipStream_t s) {
+  if (a.H % 4 == 0) {
+    const int nch = (a.H / 4 + 63) / 64;
+    if (nch <= 1) return emb_launch<T, 1, 4>(a, s);
+    if (nch <= 3) return emb_launch<T, 3, 4>(a, s);
+    if (nch <= 4) return emb_launch<T, 4, 4>(a, s);
+    if (nch <= 8) return emb_launch<T, 8, 4>(a, s);
+    if (nch <= 16) return emb_launch<T, 16, 4>(a, s);
+    return hipErrorInvalidValue;
+  }
+  const int nch = (a.H + 63) / 64;
+  if (nch <= 8) return emb_launch<T, 8, 1>(a, s);
+  if (nch <= 32) return emb_launch<T, 32, 1>(a, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,
+                           const void* pos_table, const void* type_table, int T_, int H,
+                           const float* gamma, const float* beta, float eps, int vocab,
+                           int* bad_id, void* out, hipStream_t stream) {
+  if (T_ <= 0) return hipSuccess;
+  const EmbArgs a{ids, pos_ids, word, pos_table, type_table, T_, H, gamma, beta, eps, vocab,
+                  bad_id, out};
+  switch (dtype) {
+    case F32: return emb_typed<float>(a, stream);
+    case F16: return emb_typed<_Float16>(a, stream);
+    case BF16: return emb_typed<__bf16>(a, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fl

@@ -1,0 +1,230 @@
+"""GPU parity of the model-level forward (BertModel.ForwardBatch,
+internal/embeddings/model/bert.go:149-169) against the CPU oracle on
+BASELINE.json's five configurations.
+
+Bars: fp32 (reference math on the GPU): per-vector cosine >= 0.99999 and
+max-abs <= 1e-4; fp16: cosine >= 0.999 against the CPU fp32 oracle.  Full-size
+batches run on the GPU; the oracle checks a sample of their sequences (every
+sequence is computed independently, so a row of the full batch must equal the
+oracle's result for that sequence alone)."""
+import functools
+import sys
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+synth = sys.modules["longbow_fletcher_amd"].synth
+
+COS_F32, MAXABS_F32, COS_F16 = 0.99999, 1e-4, 0.999
+
+
+def cosines(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1) + 1e-30)
+
+
+@functools.lru_cache(maxsize=None)
+def weights_for(cfg):
+    return synth.make_weights(cfg)
+
+
+def log(msg):
+    print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
+
+
+def run_gpu(fl, ctx, cfg, dtype, math_mode, ids, lengths, pool=None):
+    m = fl.Model(ctx, cfg, dtype=dtype, math=math_mode, pool=pool)
+    try:
+        m.load(weights_for(cfg))
+        out = m.forward(ids, lengths)
+        nan, bad = m.status()
+        assert not nan and not bad
+        return out
+    finally:
+        m.close()
+
+
+def sample_rows(lengths, k):
+    """k sequence indices spread over the batch (first, last, longest, shortest...)."""
+    n = len(lengths)
+    pick = {0, n - 1, int(np.argmax(lengths)), int(np.argmin(lengths))}
+    pick |= set(np.linspace(0, n - 1, k).astype(int).tolist())
+    return sorted(pick)[:max(k, 4)]
+
+
+def oracle_rows(orc, cfg, ids, lengths, rows, math_mode=0):
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    sub_ids = np.concatenate([ids[starts[r]:starts[r] + lengths[r]] for r in rows])
+    orc.set_threads(8)
+    return orc.forward(cfg, weights_for(cfg), sub_ids, np.asarray(lengths)[rows], math_mode)
+
+
+def test_config1_bert_tiny_f32_full(ctx, fl, orc):
+    """Config 1: bert-tiny, B32 x S128, fp32, mean-pool + L2 (whole batch vs oracle)."""
+    w = synth.WORKLOADS["bert-tiny-b32-s128-f32"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    log("config1 gpu")
+    got = run_gpu(fl, ctx, w.cfg, fl.F32, fl.MATH_REFERENCE, ids, lengths)
+    want = orc.forward(w.cfg, weights_for(w.cfg), ids, lengths)
+    c = cosines(got, want)
+    err = np.abs(got - want).max()
+    log(f"config1 min cos {c.min():.9f} max abs {err:.3e}")
+    assert c.min() >= COS_F32 and err <= MAXABS_F32
+
+
+def test_config1_cls_tanh_pooler(ctx, fl, orc):
+    """The reference's own output: tanh(CLS * Wp + bp) (bert.go:441-488)."""
+    w = synth.WORKLOADS["bert-tiny-b32-s128-f32"]
+    lengths = np.array([128, 5, 77, 128, 31], np.int64)
+    ids = synth.make_ids(lengths)
+    got = run_gpu(fl, ctx, w.cfg, fl.F32, fl.MATH_REFERENCE, ids, lengths,
+                  pool=fl.POOL_CLS_TANH)
+    want = orc.forward(w.cfg, weights_for(w.cfg), ids, lengths, pool=0)
+    assert np.abs(got - want).max() <= MAXABS_F32 and cosines(got, want).min() >= COS_F32
+
+
+def test_nomic_arch_f32_reference_math(ctx, fl, orc):
+    """Nomic-style architecture (RoPE base 1000, SwiGLU, no bias) in fp32, 2 layers."""
+    cfg = synth.nomic(layers=2)
+    lengths = np.array([512, 300, 64, 9], np.int64)
+    ids = synth.make_ids(lengths)
+    got = run_gpu(fl, ctx, cfg, fl.F32, fl.MATH_REFERENCE, ids, lengths)
+    want = orc.forward(cfg, weights_for(cfg), ids, lengths)
+    c, err = cosines(got, want), np.abs(got - want).max()
+    log(f"nomic f32 min cos {c.min():.9f} max abs {err:.3e}")
+    assert c.min() >= COS_F32 and err <= MAXABS_F32
+
+
+def test_config2_bert_base_f16(ctx, fl, orc):
+    """Config 2: BERT-base, B256 x S128, fp16, mean-pool (no L2)."""
+    w = synth.WORKLOADS["bert-base-b256-s128-f16"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    log("config2 gpu")
+    got = run_gpu(fl, ctx, w.cfg, fl.F16, fl.MATH_EXACT, ids, lengths)
+    rows = sample_rows(lengths, 4)
+    want = oracle_rows(orc, w.cfg, ids, lengths, rows)
+    c = cosines(got[rows], want)
+    log(f"config2 min cos {c.min():.6f}")
+    assert c.min() >= COS_F16
+    assert np.isfinite(got).all()
+
+
+def test_config3_nomic_f16(ctx, fl, orc):
+    """Config 3 (the north-star workload): Nomic, B256 x S512, fp16."""
+    w = synth.WORKLOADS["nomic-b256-s512-f16"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    log("config3 gpu")
+    got = run_gpu(fl, ctx, w.cfg, fl.F16, fl.MATH_EXACT, ids, lengths)
+    rows = sample_rows(lengths, 2)[:2]
+    want = oracle_rows(orc, w.cfg, ids, lengths, rows)
+    c = cosines(got[rows], want)
+    log(f"config3 min cos {c.min():.6f}")
+    assert c.min() >= COS_F16
+    np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+
+
+def test_config4_ragged_f16(ctx, fl, orc):
+    """Config 4: ragged B512 (log-normal lengths), right-padded input with a mask."""
+    w = synth.WORKLOADS["nomic-ragged-b512-f16"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    smax = int(lengths.max())
+    padded = np.zeros((len(lengths), smax), np.int64)
+    mask = np.zeros_like(padded)
+    off = 0
+    for b, L in enumerate(lengths):
+        padded[b, :L] = ids[off:off + L]
+        mask[b, :L] = 1
+        off += L
+    m = fl.Model(ctx, w.cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(weights_for(w.cfg))
+        got = m.forward_padded(padded, mask)
+        packed = m.forward(ids, lengths)
+    finally:
+        m.close()
+    np.testing.assert_array_equal(got, packed)
+    rows = sample_rows(lengths, 6)
+    want = oracle_rows(orc, w.cfg, ids, lengths, rows)
+    c = cosines(got[rows], want)
+    log(f"config4 lengths {lengths.min()}..{lengths.max()} min cos {c.min():.6f}")
+    assert c.min() >= COS_F16
+
+
+def test_config5_long_context_f16(ctx, fl, orc):
+    """Config 5: B16 x S8192.  Full 12-layer batch on the GPU (finite, unit
+    norm, row 0 equal to a batch of one); 1-layer parity against the oracle at
+    the full 8192 length."""
+    w = synth.WORKLOADS["nomic-b16-s8192-f16"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    m = fl.Model(ctx, w.cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(weights_for(w.cfg))
+        log("config5 gpu full batch")
+        got = m.forward(ids, lengths)
+        one = m.forward(ids[:lengths[0]], lengths[:1])
+    finally:
+        m.close()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+    assert cosines(one, got[:1]).min() >= 0.99999
+
+    cfg1 = synth.nomic(layers=1)
+    got1 = run_gpu(fl, ctx, cfg1, fl.F16, fl.MATH_EXACT, ids[:8192], np.array([8192]))
+    log("config5 oracle, 1 layer x 8192")
+    want1 = orc.forward(cfg1, weights_for(cfg1), ids[:8192], np.array([8192]))
+    c = cosines(got1, want1)
+    log(f"config5 1-layer cos {c.min():.6f}")
+    assert c.min() >= COS_F16
+
+
+def test_bf16_model(ctx, fl, orc):
+    cfg = synth.nomic(layers=2)
+    lengths = np.array([256, 40], np.int64)
+    ids = synth.make_ids(lengths)
+    got = run_gpu(fl, ctx, cfg, fl.BF16, fl.MATH_EXACT, ids, lengths)
+    want = orc.forward(cfg, weights_for(cfg), ids, lengths)
+    assert cosines(got, want).min() >= 0.995
+
+
+def test_forward_device_matches_host(ctx, fl):
+    cfg = synth.bert_tiny()
+    lengths = np.array([16, 9, 30], np.int64)
+    ids = synth.make_ids(lengths)
+    m = fl.Model(ctx, cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(weights_for(cfg))
+        host = m.forward(ids, lengths)
+        d_ids = ctx.int32(ids)
+        d_out = ctx.empty((3, cfg.hidden))
+        m.forward_device(d_ids, lengths, d_out)
+        ctx.synchronize()
+        np.testing.assert_array_equal(d_out.numpy(), host)
+        # Rows are independent of their batch neighbours.
+        solo = m.forward(ids[:16], lengths[:1])
+        assert cosines(solo, host[:1]).min() >= 0.99999
+    finally:
+        m.close()
+
+
+def test_model_errors(ctx, fl):
+    cfg = synth.bert_tiny()
+    m = fl.Model(ctx, cfg, dtype=fl.F32, math=fl.MATH_REFERENCE)
+    try:
+        with pytest.raises(fl.FletcherError):
+            m.forward(np.array([101, 40000, 102]), np.array([3]))  # id out of range
+        with pytest.raises(fl.FletcherError):
+            m.forward(np.array([101, 102]), np.array([2, 0]))      # empty sequence
+        with pytest.raises(fl.FletcherError):
+            m.set_weight("q_w.7", np.zeros(128 * 128))             # no such layer
+        with pytest.raises(fl.FletcherError):
+            m.set_weight("q_w.0", np.zeros(5))                      # wrong size
+    finally:
+        m.close()

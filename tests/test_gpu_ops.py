@@ -1,0 +1,317 @@
+"""GPU parity of the per-op C ABI (the Tensor methods of
+internal/device/device.go) against the CPU oracle, plus the reference's own
+known-answer tests (internal/device/device_test.go, cast_test.go,
+attention_test.go) re-run through the HIP backend."""
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(20261201)
+
+
+def rand(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def close(got, want, atol, rtol=0.0):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bound = atol + rtol * np.abs(want)
+    assert np.all(err <= bound), f"max err {err.max():.3e} (atol {atol}, rtol {rtol})"
+
+
+# ---- device_test.go known answers -------------------------------------------
+def test_known_add(ctx, fl):
+    a = ctx.tensor(np.array([[1, 2], [3, 4]], np.float32))
+    b = ctx.tensor(np.array([[10, 20], [30, 40]], np.float32))
+    ctx.add(a, b)
+    close(a.numpy().ravel(), [11, 22, 33, 44], 1e-6)
+
+
+def test_known_mul(ctx, fl):
+    # device_test.go:27-54: [2x3]*[3x2] = [58, 64, 139, 154]
+    a = ctx.tensor(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
+    b = ctx.tensor(np.array([[7, 8], [9, 10], [11, 12]], np.float32))
+    close(ctx.gemm(a, b).numpy().ravel(), [58, 64, 139, 154], 1e-6)
+
+
+def test_known_scale(ctx, fl):
+    a = ctx.tensor(np.array([[1, 2], [3, 4]], np.float32))
+    ctx.scale(a, 2.0)
+    close(a.numpy().ravel(), [2, 4, 6, 8], 1e-6)
+
+
+def test_known_layernorm(ctx, fl):
+    # device_test.go:69-96 (eps 1e-6, tolerance 1e-4)
+    a = ctx.tensor(np.array([[1, 2, 3, 4]], np.float32))
+    g = ctx.tensor(np.ones(4, np.float32))
+    b = ctx.tensor(np.zeros(4, np.float32))
+    ctx.layernorm(a, g, b, 1e-6)
+    close(a.numpy().ravel(), [-1.3416407, -0.4472136, 0.4472136, 1.3416407], 1e-4)
+
+
+def test_get_tensor_zeroed(ctx, fl):
+    # device_test.go:98-112: a pooled tensor comes back zeroed.
+    t = ctx.empty((10, 10))
+    ctx.add_scalar(t, 123.0)
+    t.free()
+    t2 = ctx.empty((10, 10))
+    assert float(np.abs(t2.numpy()).max()) == 0.0
+
+
+def test_known_cast(ctx, fl):
+    # cast_test.go:11-47: 1.0 -> 0x3c00, -2.0 -> 0xc000
+    t = ctx.tensor(np.array([[1.0, -2.0]], np.float32))
+    h = ctx.cast(t, fl.F16).raw().ravel()
+    assert int(h[0]) == 0x3C00 and int(h[1]) == 0xC000
+
+
+def test_truncating_upload_matches_utils_go(ctx, fl, orc):
+    vals = np.concatenate([rand(4000, scale=3.0), rand(1000, scale=1e-4),
+                           np.array([7e4, -7e4, 65504, 6e-5, -6e-5, 0.0, 1.0, -2.0, 3.14159],
+                                    np.float32)])
+    t = ctx.tensor(vals, fl.F16, rounding=fl.ROUND_TRUNCATE)
+    want = np.array([orc.f32_to_f16_bits(v) for v in vals], np.uint16)
+    np.testing.assert_array_equal(t.raw().ravel(), want)
+
+
+# ---- GEMM / Linear -----------------------------------------------------------
+@pytest.mark.parametrize("m,k,n", [(512, 128, 384), (300, 256, 128), (37, 64, 64), (5, 7, 3)])
+def test_gemm_f32_vs_openblas(ctx, fl, orc, m, k, n):
+    a, b = rand(m, k), rand(k, n)
+    got = ctx.gemm(ctx.tensor(a), ctx.tensor(b)).numpy()
+    close(got, orc.mul(a, b), 2e-5 * math.sqrt(k), 1e-5)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (1, 1)])
+def test_gemm_transposes(ctx, fl, orc, ta, tb):
+    a = rand(64, 96) if not ta else rand(96, 64)
+    b = rand(96, 128) if not tb else rand(128, 96)
+    got = ctx.gemm(ctx.tensor(a), ctx.tensor(b), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    close(got, orc.mul(a, b, bool(ta), bool(tb)), 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("m,k,n", [(1024, 768, 768), (333, 768, 2304), (256, 3072, 768)])
+def test_gemm_16bit(ctx, fl, orc, dtype, m, k, n):
+    dt = fl.F16 if dtype == "f16" else fl.BF16
+    a, b = rand(m, k), rand(k, n, scale=0.05)
+    da, db = ctx.tensor(a, dt), ctx.tensor(b, dt)
+    ar, br = da.numpy(), db.numpy()  # exactly the rounded operands
+    want = orc.mul(ar, br)
+    got = ctx.gemm(da, db).numpy()
+    ulp = 2 ** -10 if dt == fl.F16 else 2 ** -7
+    close(got, want, 2 * ulp * np.abs(want).max() + 1e-3, 2 * ulp)
+
+
+@pytest.mark.parametrize("act", ["identity", "gelu", "tanh", "softmax", "swiglu"])
+def test_linear_f32_reference_math(ctx, fl, orc, act):
+    a_id = {"identity": 0, "gelu": 1, "tanh": 2, "softmax": 3, "swiglu": 4}[act]
+    x, w, b = rand(200, 128), rand(128, 256, scale=0.1), rand(256, scale=0.1)
+    got = ctx.linear(ctx.tensor(x), ctx.tensor(w), ctx.tensor(b), act=a_id,
+                     math=fl.MATH_REFERENCE).numpy()
+    want = orc.linear_activation(x, w, b, a_id)
+    close(got, want, 1e-5, 1e-5)
+
+
+def test_linear_out_in_layout(ctx, fl, orc):
+    x, w = rand(130, 256), rand(256, 192, scale=0.1)
+    got = ctx.linear(ctx.tensor(x), ctx.tensor(np.ascontiguousarray(w.T)),
+                     w_layout=fl.W_OUT_IN).numpy()
+    close(got, orc.linear(x, w), 1e-5, 1e-5)
+
+
+def test_linear_swiglu_identity_trick(ctx, fl):
+    # swiglu_test.go:11-142: X = I, W = data, so LinearActivation = SwiGLU(data).
+    n, inter = 10, 128
+    data = (np.arange(n * 2 * inter) % 100 / 10.0).astype(np.float32).reshape(n, 2 * inter)
+    x = np.eye(n, dtype=np.float32)
+    got = ctx.linear(ctx.tensor(x), ctx.tensor(data), ctx.tensor(np.zeros(2 * inter, np.float32)),
+                     act=fl.ACT_SWIGLU).numpy()
+    g, u = data[:, :inter].astype(np.float64), data[:, inter:].astype(np.float64)
+    close(got, g / (1 + np.exp(-g)) * u, 1e-4, 1e-6)
+
+
+# ---- elementwise / norm --------------------------------------------------------
+def test_add_bias_scale_addscalar(ctx, fl, orc):
+    t, b = rand(33, 70), rand(70)
+    d = ctx.tensor(t)
+    ctx.add_bias(d, ctx.tensor(b))
+    ctx.scale(d, 0.37)
+    ctx.add_scalar(d, -1.25)
+    want = orc.scale(orc.add_bias(t, b), 0.37) - np.float32(1.25)
+    close(d.numpy(), want, 1e-6)
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+def test_activation_reference_math(ctx, fl, orc, act):
+    t = rand(64, 300, scale=3.0)
+    d = ctx.tensor(t)
+    ctx.activation(d, act, fl.MATH_REFERENCE)
+    if act == 1:
+        want = orc.gelu_fast(t)
+    elif act == 2:
+        want = orc.tanh(t)
+    else:
+        want = orc.softmax_rows(t)
+    close(d.numpy(), want, 2e-6, 2e-6)
+
+
+@pytest.mark.parametrize("cols", [128, 768, 100, 1000])
+def test_add_layernorm_f32(ctx, fl, orc, cols):
+    t, r = rand(257, cols), rand(257, cols)
+    g, b = rand(cols) + 1.0, rand(cols)
+    d = ctx.tensor(t)
+    ctx.add_layernorm(d, ctx.tensor(r), ctx.tensor(g), ctx.tensor(b), 1e-7)
+    close(d.numpy(), orc.add_layernorm(t, r, g, b, 1e-7), 2e-5, 1e-5)
+
+
+def test_layernorm_f16(ctx, fl, orc):
+    t = rand(512, 768)
+    d = ctx.tensor(t, fl.F16)
+    g, b = np.ones(768, np.float32), np.zeros(768, np.float32)
+    want = orc.layernorm(d.numpy(), g, b, 1e-7)
+    ctx.layernorm(d, ctx.tensor(g), ctx.tensor(b), 1e-7)
+    close(d.numpy(), want, 4e-3, 2e-3)
+
+
+def test_gather_and_bounds(ctx, fl, orc):
+    table = rand(100, 48)
+    idx = RNG.integers(0, 100, 77)
+    got = ctx.gather(ctx.tensor(table), idx).numpy()
+    np.testing.assert_array_equal(got, orc.gather(table, idx))
+    with pytest.raises(fl.FletcherError):
+        ctx.gather(ctx.tensor(table), [0, 100])
+
+
+def test_slice(ctx, fl):
+    t = rand(20, 30)
+    got = ctx.slice(ctx.tensor(t), 3, 11, 5, 29).numpy()
+    np.testing.assert_array_equal(got, t[3:11, 5:29])
+    with pytest.raises(fl.FletcherError):
+        ctx.slice(ctx.tensor(t), 5, 5, 0, 3)
+
+
+def test_has_nan(ctx, fl):
+    t = rand(1000, 17)
+    assert not ctx.has_nan(ctx.tensor(t))
+    t[512, 3] = np.inf
+    assert ctx.has_nan(ctx.tensor(t))
+    t[512, 3] = np.nan
+    assert ctx.has_nan(ctx.tensor(t, fl.F16))
+
+
+# ---- RoPE ------------------------------------------------------------------------
+@pytest.mark.parametrize("base", [10000.0, 1000.0])
+def test_rope_f32_vs_oracle(ctx, fl, orc, base):
+    b, s, heads, hd = 2, 128, 4, 64  # rope_test.go:15-18 shape
+    t = rand(b * s, heads * hd)
+    d = ctx.tensor(t)
+    ctx.rope(d, b, s, heads, hd, base)
+    close(d.numpy(), orc.rope(t, b, s, heads, hd, base), 1e-6, 1e-6)
+
+
+def test_rope_varlen_positions_restart(ctx, fl, orc):
+    lengths = [5, 17, 64]
+    t = rand(sum(lengths), 2 * 64)
+    d = ctx.tensor(t)
+    ctx.rope_varlen(d, lengths, 2, 64, 1000.0)
+    want, off = [], 0
+    for L in lengths:
+        want.append(orc.rope(t[off:off + L], 1, L, 2, 64, 1000.0))
+        off += L
+    close(d.numpy(), np.concatenate(want), 1e-6, 1e-6)
+
+
+# ---- attention ---------------------------------------------------------------------
+def test_attention_reference_test_inputs(ctx, fl):
+    # attention_test.go:70-125: B1 S4 heads2 d4, q=i*0.1, k=(n-i)*0.1, v=(i%3)*0.5,
+    # naive exact-exp attention, MSE <= 1e-3.
+    n = 4 * 8
+    q = (np.arange(n) * 0.1).astype(np.float32).reshape(4, 8)
+    k = ((n - np.arange(n)) * 0.1).astype(np.float32).reshape(4, 8)
+    v = ((np.arange(n) % 3) * 0.5).astype(np.float32).reshape(4, 8)
+    scale = 1 / math.sqrt(4)
+    want = np.zeros((4, 8))
+    for h in range(2):
+        qh, kh, vh = (x[:, h * 4:(h + 1) * 4].astype(np.float64) for x in (q, k, v))
+        s = qh @ kh.T * scale
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        want[:, h * 4:(h + 1) * 4] = p @ vh
+    for dt in (fl.F32, fl.F16):
+        got = ctx.attention(ctx.tensor(q, dt), ctx.tensor(k, dt), ctx.tensor(v, dt), 1, 4, 2, scale,
+                            fl.MATH_EXACT).numpy()
+        assert float(np.mean((got - want) ** 2)) <= 1e-3
+
+
+@pytest.mark.parametrize("seq", [128, 77, 300])
+def test_attention_f32_reference_math(ctx, fl, orc, seq):
+    b, heads = 3, 2
+    q, k, v = (rand(b * seq, heads * 64) for _ in range(3))
+    got = ctx.attention(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), b, seq, heads, 0.125,
+                        fl.MATH_REFERENCE).numpy()
+    close(got, orc.attention(q, k, v, b, seq, heads, 0.125), 2e-5, 1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("seq", [512, 100, 1, 65])
+def test_attention_flash_16bit(ctx, fl, orc, dtype, seq):
+    dt = fl.F16 if dtype == "f16" else fl.BF16
+    b, heads = 2, 3
+    q, k, v = (rand(b * seq, heads * 64) for _ in range(3))
+    dq, dk, dv = ctx.tensor(q, dt), ctx.tensor(k, dt), ctx.tensor(v, dt)
+    qr, kr, vr = dq.numpy(), dk.numpy(), dv.numpy()
+    want = np.zeros_like(qr, dtype=np.float64)
+    for bi in range(b):
+        for h in range(heads):
+            rs, cs = slice(bi * seq, (bi + 1) * seq), slice(h * 64, (h + 1) * 64)
+            s = qr[rs, cs].astype(np.float64) @ kr[rs, cs].astype(np.float64).T * 0.125
+            p = np.exp(s - s.max(1, keepdims=True))
+            want[rs, cs] = (p / p.sum(1, keepdims=True)) @ vr[rs, cs]
+    got = ctx.attention(dq, dk, dv, b, seq, heads, 0.125, fl.MATH_EXACT).numpy()
+    tol = 4e-3 if dt == fl.F16 else 3e-2
+    close(got, want, tol, tol)
+
+
+def test_attention_varlen_equals_per_sequence(ctx, fl, orc):
+    lengths = [7, 64, 129, 1, 300]
+    heads, hd = 2, 64
+    T = sum(lengths)
+    q, k, v = (rand(T, heads * hd) for _ in range(3))
+    got = ctx.attention_varlen(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), lengths, heads, 0.125,
+                               fl.MATH_REFERENCE).numpy()
+    close(got, orc.attention_varlen(q, k, v, lengths, heads, 0.125), 2e-5, 1e-5)
+    got16 = ctx.attention_varlen(ctx.tensor(q, fl.F16), ctx.tensor(k, fl.F16),
+                                 ctx.tensor(v, fl.F16), lengths, heads, 0.125,
+                                 fl.MATH_EXACT).numpy()
+    close(got16, got, 1e-2, 1e-2)
+
+
+def test_attention_generic_head_dim(ctx, fl, orc):
+    b, s, heads = 2, 33, 3  # head_dim 32: generic kernel
+    q, k, v = (rand(b * s, heads * 32) for _ in range(3))
+    got = ctx.attention(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), b, s, heads,
+                        1 / math.sqrt(32), fl.MATH_REFERENCE).numpy()
+    close(got, orc.attention(q, k, v, b, s, heads, 1 / math.sqrt(32)), 2e-5, 1e-5)
+
+
+# ---- pooling -------------------------------------------------------------------------
+def test_mean_pool_l2(ctx, fl):
+    lengths = [1, 64, 65, 200]
+    h = rand(sum(lengths), 768)
+    got = ctx.mean_pool(ctx.tensor(h), lengths, l2=True).numpy()
+    off, want = 0, []
+    for L in lengths:
+        p = h[off:off + L].astype(np.float64).mean(0)
+        want.append(p / max(np.linalg.norm(p), 1e-12))
+        off += L
+    close(got, np.array(want), 1e-6, 1e-5)
+    close(np.linalg.norm(got, axis=1), np.ones(len(lengths)), 1e-6)
