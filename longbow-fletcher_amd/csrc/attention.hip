@@ -286,13 +286,13 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
 
   const int qr = w.q0 + wave * 16 + lrow;
   // Chunk dc covers d in [16*dc, 16*dc+16); lane group g holds d = 16*dc + 4g + j.
-  u32x4_t qf[4];
+  float4_t qf[4];
 #pragma unroll
   for (int dc = 0; dc < 4; ++dc) {
     if (qr < L)
-      qf[dc] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + dc * 16 + lgrp * 4);
+      qf[dc] = *(const float4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + dc * 16 + lgrp * 4);
     else
-      qf[dc] = u32x4_t{0, 0, 0, 0};
+      qf[dc] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
 
   auto load_tile = [&](int kv0, bool with_v) {
@@ -315,12 +315,11 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
       s[kt] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
-        const u32x4_t kf = *(const u32x4_t*)(&Ks[(kt * 16 + lrow) * S + dc * 16 + lgrp * 4]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, kf[j]),
-                                                       __builtin_bit_cast(float, qf[dc][j]),
-                                                       s[kt], 0, 0, 0);
+        const float4_t kf = *(const float4_t*)(&Ks[(kt * 16 + lrow) * S + dc * 16 + lgrp * 4]);
+        s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[0], qf[dc][0], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[1], qf[dc][1], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[2], qf[dc][2], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[3], qf[dc][3], s[kt], 0, 0, 0);
       }
     }
   };
@@ -338,7 +337,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (kv0 + kt * 16 + lgrp * 4 + i < L) mx = fmaxf(mx, s[kt][i] * scale);
+        if (kv0 + kt * 16 + lgrp * 4 + i < L) mx = fmaxf(mx, mul_rn(s[kt][i], scale));
     __syncthreads();
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -361,7 +360,7 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
       for (int i = 0; i < 4; ++i) {
         float e = 0.f;
         if (kv0 + kt * 16 + lgrp * 4 + i < L) {
-          const float sc = s[kt][i] * scale;
+          const float sc = mul_rn(s[kt][i], scale);
           if constexpr (MATH == MATH_REFERENCE) e = exp_fast_ref(sc - mx);
           else e = expf(sc - mx);
         }
@@ -425,14 +424,15 @@ attn_generic_kernel(const T* q, const T* k, const T* v, int ld, T* out, int ldo,
     const T* krow = k + (size_t)(s0 + j) * ld + h * hd;
     float acc = 0.f;
     for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
-    mx = fmaxf(mx, acc * scale);
+    mx = fmaxf(mx, mul_rn(acc, scale));
   }
   float sum = 0.f;
   for (int j = 0; j < L; ++j) {
     const T* krow = k + (size_t)(s0 + j) * ld + h * hd;
     float acc = 0.f;
     for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
-    sum += MATH == MATH_REFERENCE ? exp_fast_ref(acc * scale - mx) : expf(acc * scale - mx);
+    const float sc = mul_rn(acc, scale);
+    sum += MATH == MATH_REFERENCE ? exp_fast_ref(sc - mx) : expf(sc - mx);
   }
   const float inv = 1.0f / sum;
   T* orow = out + (size_t)(s0 + qi) * ldo + h * hd;
@@ -445,8 +445,8 @@ attn_generic_kernel(const T* q, const T* k, const T* v, int ld, T* out, int ldo,
       const T* vrow = v + (size_t)(s0 + j) * ld + h * hd;
       float acc = 0.f;
       for (int d = 0; d < hd; ++d) acc += to_f(qrow[d]) * to_f(krow[d]);
-      const float pr =
-          (MATH == MATH_REFERENCE ? exp_fast_ref(acc * scale - mx) : expf(acc * scale - mx)) * inv;
+      const float sc = mul_rn(acc, scale);
+      const float pr = (MATH == MATH_REFERENCE ? exp_fast_ref(sc - mx) : expf(sc - mx)) * inv;
       for (int d = 0; d < dn; ++d) o[d] += pr * to_f(vrow[d0 + d]);
     }
     for (int d = 0; d < dn; ++d) orow[d0 + d] = from_f<T>(o[d]);

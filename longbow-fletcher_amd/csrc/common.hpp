@@ -73,6 +73,15 @@ __device__ inline float exp_fast_ref(float x) {
   return p * ldexpf(1.0f, k);
 }
 
+// A float32 product that is never fused into a following add: the reference
+// scales scores (sgemm alpha) and subtracts the row max as two rounded
+// operations, and ExpFast's floor step turns a fused residue below zero into a
+// 0.56% jump, so the rounding must match.
+__device__ inline float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 // simd.go:49-64 TanhFast.
 __device__ inline float tanh_fast_ref(float x) {
 #pragma clang fp contract(off)

@@ -35,10 +35,12 @@ template <> struct Mfma<float> {
   // Four k=4 steps; lane group g supplies k = 4g + j at step j for both
   // operands, so the sum covers the 16 k values of the fragment.
   __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a[j]),
-                                               __builtin_bit_cast(float, b[j]), c, 0, 0, 0);
+    const float4_t af = __builtin_bit_cast(float4_t, a);
+    const float4_t bf = __builtin_bit_cast(float4_t, b);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], c, 0, 0, 0);
   }
 };
 
