@@ -31,9 +31,15 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object
           "-Wall", "-Wno-unused-function", f"-I{ROOT / 'include'}"]
 
 
+# Per-file flags.  gemm.hip: keep MFMA accumulators in architectural VGPRs
+# (the accumulator-register form made the allocator copy accumulators every
+# K step).
+PER_FILE = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: pathlib.Path) -> pathlib.Path:
     obj = OBJDIR / (src.name + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in (r.stderr or "").splitlines()
                      if "packed-fp32-ops" not in l)

@@ -256,22 +256,270 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_nt_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile configurations
+// 16-bit GEMM with direct global->LDS loads (global_load_lds_dwordx4).
+// Each wave instruction writes 64 lanes x 16 B = 1 KB contiguously in lane
+// order, so the LDS layout is chosen through the source address each lane
+// fetches: rows of BK = 64 halfs (128 B) unpadded, 16-byte chunk c of row r
+// stored at position c ^ swz(r) so the 16 rows of an MFMA fragment read land
+// in distinct banks.  Two statically distinct LDS stages let the compiler see
+// that reads of one stage do not alias the DMA into the other; one barrier
+// per K step.  Token rows past M are clamped to row M-1 (read, never stored).
 // ---------------------------------------------------------------------------
-template <typename T> struct TileCfg;
-template <> struct TileCfg<_Float16> {
-  static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2;
-};
-template <> struct TileCfg<__bf16> {
-  static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2;
-};
-template <> struct TileCfg<float> {
-  static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1;
-};
+template <int SWZ_SHIFT, int CPR>
+__device__ inline int lds_swz(int row) { return (row >> SWZ_SHIFT) & (CPR - 1); }
 
-template <typename T, int EPI, int MATH>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int EPI, int MATH, int SWZ_SHIFT,
+          int STAGES>
+__global__ void __launch_bounds__(WM* WN * 64) gemm_lds_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int ROWB = BK * 2;                // bytes per LDS row
+  constexpr int CPR = BK / 8;                 // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;               // rows per 1 KB wave load
+  static_assert(BK == 32 || BK == 64, "BK 32 or 64");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, FN = WTN / 16;
+  constexpr int A_INS = BM / RPI / NW, B_INS = BN / RPI / NW;  // 1 KB wave loads per stage
+  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
+  static_assert(EPI != EPI_SWIGLU || FN % 2 == 0, "SwiGLU needs gate/up tile pairs");
+  static_assert(EPI != EPI_ROPE || WTN % 64 == 0, "RoPE needs whole 64-wide heads per wave");
+  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 LDS stages");
+  __shared__ __attribute__((aligned(1024))) char lds0[(BM + BN) * ROWB];
+  __shared__ __attribute__((aligned(1024))) char lds1[(BM + BN) * ROWB];
+  __shared__ __attribute__((aligned(1024))) char lds2[STAGES == 3 ? (BM + BN) * ROWB : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
+  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * num_n;
+  const int g = L / per_group;
+  const int first_m = g * GROUP_M;
+  const int gsize = min(num_m - first_m, GROUP_M);
+  const int r = L - g * per_group;
+  const int m0 = (first_m + r % gsize) * BM;
+  const int n0 = (r / gsize) * BN;
+  const int M = p.M;
+
+  // Per-lane 32-bit byte offsets from wave-uniform tile bases, so the loads
+  // use the scalar-base + vector-offset form (one VGPR each).
+  const char* abase = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
+  const char* bbase = (const char*)p.B + (size_t)n0 * p.ldb * sizeof(T);
+  uint32_t aoff[A_INS], boff[B_INS];
+#pragma unroll
+  for (int i = 0; i < A_INS; ++i) {
+    const int row = (wave * A_INS + i) * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ lds_swz<SWZ_SHIFT, CPR>(row);
+    const int rr = min(row, M - 1 - m0);
+    aoff[i] = (uint32_t)(rr * p.lda + c * 8) * (uint32_t)sizeof(T);
+  }
+#pragma unroll
+  for (int i = 0; i < B_INS; ++i) {
+    const int row = (wave * B_INS + i) * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ lds_swz<SWZ_SHIFT, CPR>(row);
+    boff[i] = (uint32_t)(row * p.ldb + c * 8) * (uint32_t)sizeof(T);
+  }
+  auto issue = [&](char* stage, int k0) {
+    const char* ak = abase + (size_t)k0 * sizeof(T);
+    const char* bk = bbase + (size_t)k0 * sizeof(T);
+#pragma unroll
+    for (int i = 0; i < A_INS; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(ak + aoff[i]),
+          (__attribute__((address_space(3))) void*)(stage + (wave * A_INS + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_INS; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(bk + boff[i]),
+          (__attribute__((address_space(3))) void*)(stage + BM * ROWB + (wave * B_INS + i) * 1024),
+          16, 0, 0);
+  };
+
+  // Fragment read offsets: row = base + t*16 + (lane & 15); swz depends on lane only.
+  const int fr = lane & 15, fg = lane >> 4;
+  const int swz = lds_swz<SWZ_SHIFT, CPR>(fr);
+  const int a_row0 = (wm * WTM + fr) * ROWB;
+  const int b_row0 = BM * ROWB + (wn * WTN + fr) * ROWB;
+
+  float4_t acc[FN][TM];
+#pragma unroll
+  for (int f = 0; f < FN; ++f)
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[f][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const char* stage) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      const int co = ((ks * 4 + fg) ^ swz) << 4;
+      u32x4_t fa[TM], fb[FN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) fa[t] = *(const u32x4_t*)(stage + a_row0 + t * 16 * ROWB + co);
+#pragma unroll
+      for (int f = 0; f < FN; ++f) fb[f] = *(const u32x4_t*)(stage + b_row0 + f * 16 * ROWB + co);
+#pragma unroll
+      for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int t = 0; t < TM; ++t) Mfma<T>::mma(acc[f][t], fb[f], fa[t]);
+      // Keep one K substep's fragments live at a time.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // K is a multiple of STAGES*BK (checked on the host), so stages rotate
+  // without a mid-loop exit (which would make every accumulator a loop-exit
+  // value).  Loads of the last iterations re-fetch tile 0 into an idle stage
+  // (in bounds, never read) to keep the wait counts uniform.  vmcnt counts
+  // in issue order: waiting for <= one stage of loads outstanding means the
+  // oldest stage has landed.
+  const int nk = p.K / BK;
+  auto kclamp = [&](int k) { return (k < nk ? k : 0) * BK; };
+  if constexpr (STAGES == 2) {
+    issue(lds0, 0);
+    for (int kt = 0; kt < nk; kt += 2) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      issue(lds1, kclamp(kt + 1));
+      compute(lds0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      issue(lds0, kclamp(kt + 2));
+      compute(lds1);
+    }
+  } else {
+    constexpr int PER = A_INS + B_INS;  // loads per stage per wave
+    static_assert(PER <= 63, "vmcnt range");
+    issue(lds0, 0);
+    issue(lds1, kclamp(1));
+    for (int kt = 0; kt < nk; kt += 3) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+      __syncthreads();
+      issue(lds2, kclamp(kt + 2));
+      compute(lds0);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+      __syncthreads();
+      issue(lds0, kclamp(kt + 3));
+      compute(lds1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+      __syncthreads();
+      issue(lds1, kclamp(kt + 4));
+      compute(lds2);
+    }
+  }
+  // No DMA may still target this workgroup's LDS when it exits.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  T* C = (T*)p.C;
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int nbase = n0 + wn * WTN;
+  const float* bias = p.epi.bias;
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int m = m0 + wm * WTM + t * 16 + lrow;
+    if (m >= M) continue;
+    T* crow = C + (size_t)m * p.ldc;
+    if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int j = 0; j < FN / 2; ++j) {
+        const int ng = nbase + 2 * j * 16 + lgrp * 4;
+        float4_t gt = acc[2 * j][t], up = acc[2 * j + 1][t];
+        if (bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            gt[i] += bias[ng + i];
+            up[i] += bias[ng + 16 + i];
+          }
+        }
+        float4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = silu_m<MATH>(gt[i]) * up[i];
+        store4<T>(crow + nbase / 2 + j * 16 + lgrp * 4, o);
+      }
+    } else if constexpr (EPI == EPI_ROPE) {
+      const int ps = p.epi.pos[m];
+      const float2* cs = p.epi.rope_cs + (size_t)ps * 32;
+#pragma unroll
+      for (int h = 0; h < FN / 4; ++h) {
+        const int hb = nbase + h * 64;
+        float4_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = acc[h * 4 + q][t];
+          if (bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[q][i] += bias[hb + q * 16 + lgrp * 4 + i];
+          }
+        }
+        if (hb < p.epi.rope_cols) {
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float2 c = cs[q * 16 + lgrp * 4 + i];
+              const float x1 = v[q][i], x2 = v[q + 2][i];
+              v[q][i] = x1 * c.x - x2 * c.y;
+              v[q + 2][i] = x1 * c.y + x2 * c.x;
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) store4<T>(crow + hb + q * 16 + lgrp * 4, v[q]);
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < FN; ++f) {
+        const int n = nbase + f * 16 + lgrp * 4;
+        float4_t v = acc[f][t];
+        if (bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += bias[n + i];
+        }
+        store4<T>(crow + n, act4<EPI, MATH>(v));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile configurations.  16-bit: 256x256 tiles of 4 waves x (128x128) when
+// N % 256 == 0 (4 MFMAs per 16-byte LDS fragment read, 144 KB of LDS double
+// buffered, one workgroup per CU), else 256x128 tiles of 4 x (128x64).
+// ---------------------------------------------------------------------------
+struct Cfg256x256 { static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2; };
+struct Cfg256x128 { static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2; };
+// Direct-LDS 16-bit GEMM defaults: 256x128 tiles, BK = 32, two LDS stages
+// (48 KB, so two workgroups share a CU), chunk swizzle (row >> 1) & 3.
+#ifndef FL_GEMM_SWZ
+#define FL_GEMM_SWZ 1
+#endif
+#ifndef FL_GEMM_LDS_CFG
+#define FL_GEMM_LDS_CFG 1
+#endif
+#ifndef FL_GEMM_STAGES
+#define FL_GEMM_STAGES 2
+#endif
+#ifndef FL_GEMM_BK
+#define FL_GEMM_BK 32
+#endif
+#ifndef FL_GEMM_NT_256
+#define FL_GEMM_NT_256 0
+#endif
+struct CfgF32 { static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1; };
+
+template <typename T, typename C, int EPI, int MATH>
+static hipError_t launch_lds(const GemmParams& p, hipStream_t s) {
+  const int num_m = (p.M + C::BM - 1) / C::BM;
+  const int num_n = p.N / C::BN;
+  dim3 grid(num_m * num_n), block(C::WM * C::WN * 64);
+  hipLaunchKernelGGL(
+      (gemm_lds_kernel<T, C::BM, C::BN, FL_GEMM_BK, C::WM, C::WN, EPI, MATH, FL_GEMM_SWZ,
+                       FL_GEMM_STAGES>),
+      grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, typename C, int EPI, int MATH>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
-  using C = TileCfg<T>;
   const int num_m = (p.M + C::BM - 1) / C::BM;
   const int num_n = p.N / C::BN;
   dim3 grid(num_m * num_n), block(C::WM * C::WN * 64);
@@ -280,29 +528,44 @@ static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <typename T, int EPI, int MATH>
+static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
+  if constexpr (sizeof(T) == 4) {
+    return launch_cfg<T, CfgF32, EPI, MATH>(p, s);
+  } else {
+#if FL_GEMM_LDS_CFG == 2
+    if (p.N % 256 == 0 && p.K % 128 == 0) return launch_lds<T, Cfg256x256, EPI, MATH>(p, s);
+#elif FL_GEMM_LDS_CFG == 1
+    if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
+#endif
+    if (p.N % 256 == 0 && FL_GEMM_NT_256) return launch_cfg<T, Cfg256x256, EPI, MATH>(p, s);
+    return launch_cfg<T, Cfg256x128, EPI, MATH>(p, s);
+  }
+}
+
 template <typename T>
 static hipError_t launch_typed(const GemmParams& p, hipStream_t s) {
   const bool ref = p.epi.math == MATH_REFERENCE;
   switch (p.epi.kind) {
-    case EPI_STORE: return launch_cfg<T, EPI_STORE, MATH_EXACT>(p, s);
-    case EPI_ROPE: return launch_cfg<T, EPI_ROPE, MATH_EXACT>(p, s);
+    case EPI_STORE: return launch_pick<T, EPI_STORE, MATH_EXACT>(p, s);
+    case EPI_ROPE: return launch_pick<T, EPI_ROPE, MATH_EXACT>(p, s);
     case EPI_GELU:
-      return ref ? launch_cfg<T, EPI_GELU, MATH_REFERENCE>(p, s)
-                 : launch_cfg<T, EPI_GELU, MATH_EXACT>(p, s);
+      return ref ? launch_pick<T, EPI_GELU, MATH_REFERENCE>(p, s)
+                 : launch_pick<T, EPI_GELU, MATH_EXACT>(p, s);
     case EPI_TANH:
-      return ref ? launch_cfg<T, EPI_TANH, MATH_REFERENCE>(p, s)
-                 : launch_cfg<T, EPI_TANH, MATH_EXACT>(p, s);
+      return ref ? launch_pick<T, EPI_TANH, MATH_REFERENCE>(p, s)
+                 : launch_pick<T, EPI_TANH, MATH_EXACT>(p, s);
     case EPI_SWIGLU:
-      return ref ? launch_cfg<T, EPI_SWIGLU, MATH_REFERENCE>(p, s)
-                 : launch_cfg<T, EPI_SWIGLU, MATH_EXACT>(p, s);
+      return ref ? launch_pick<T, EPI_SWIGLU, MATH_REFERENCE>(p, s)
+                 : launch_pick<T, EPI_SWIGLU, MATH_EXACT>(p, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <typename T>
 static bool cfg_ok(int N, int K) {
-  using C = TileCfg<T>;
-  return N % C::BN == 0 && K % C::BK == 0;
+  if constexpr (sizeof(T) == 4) return N % CfgF32::BN == 0 && K % CfgF32::BK == 0;
+  else return N % Cfg256x128::BN == 0 && K % Cfg256x128::BK == 0;
 }
 
 bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
