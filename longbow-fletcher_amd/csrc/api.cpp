@@ -372,6 +372,23 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
   if (m == 0 || n == 0) return FL_OK;
   GemmEpilogue epi;
   if (!trans_a && alpha == 1.0f) {
+    // The ping-pong kernel takes B packed [n x k] in its own row order.
+    const int lay = gemm_pp_layout(dtype, n, k, EPI_STORE, FL_MATH_EXACT, false);
+    const size_t esz = dtype_size(dtype);
+    const bool rows_ok = trans_b && !(((uintptr_t)b | ((size_t)ldb * esz)) & 15);
+    if (lay >= 0 && ((!trans_b && ldb == n) || rows_ok)) {
+      int st;
+      void* w = workspace(ctx, (size_t)n * k * esz, &st);
+      if (st) return st;
+      if (trans_b) FL_CHECK_LAUNCH(launch_pack_rows(dtype, b, ldb, n, k, w, lay, ctx->stream));
+      else FL_CHECK_LAUNCH(launch_transpose(dtype, b, k, n, w, lay, ctx->stream));
+      GemmEpilogue pe;
+      pe.layout = lay;
+      if (gemm_nt_supported(dtype, m, n, k, a, lda, w, k, c, ldc, pe)) {
+        FL_CHECK_LAUNCH(launch_gemm_nt(dtype, a, lda, w, k, c, ldc, m, n, k, pe, ctx->stream));
+        return FL_OK;
+      }
+    }
     const void* bnk = b;
     int ldbn = ldb;
     if (!trans_b) {
@@ -414,26 +431,40 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   const bool unfused = act == FL_ACT_SWIGLU || act == FL_ACT_SOFTMAX;
   const size_t y_bytes = unfused ? (size_t)rows * out_cols * esz : 0;
   int st;
-  char* ws = (char*)workspace(ctx, bias_bytes + w_bytes + y_bytes, &st);
+  // [packed fp32 bias][fp32 bias staging][packed W][unfused product]
+  char* ws = (char*)workspace(ctx, 2 * bias_bytes + w_bytes + y_bytes, &st);
   if (st) return st;
-  float* bias32 = nullptr;
-  if (bias) {
-    bias32 = (float*)ws;
-    FL_CHECK_LAUNCH(launch_cast(bias, dtype, bias32, FL_F32, out_cols, 0, ctx->stream));
-  }
-  void* y = unfused ? (void*)(ws + bias_bytes + w_bytes) : out;
+  void* y = unfused ? (void*)(ws + 2 * bias_bytes + w_bytes) : out;
   const int epi_act = (act == FL_ACT_GELU || act == FL_ACT_TANH) ? act : FL_ACT_IDENTITY;
 
   GemmEpilogue epi;
   epi.kind = epi_act == FL_ACT_GELU ? EPI_GELU : (epi_act == FL_ACT_TANH ? EPI_TANH : EPI_STORE);
   epi.math = math;
+  // The ping-pong kernel takes W and the bias in its own row order.
+  const int lay = gemm_pp_layout(dtype, out_cols, in_cols, epi.kind, math, bias != nullptr);
+  if (lay >= 0 && w_layout == FL_W_OUT_IN && (((uintptr_t)w | ((size_t)in_cols * esz)) & 15))
+    epi.layout = PACK_PLAIN;
+  else
+    epi.layout = lay >= 0 ? lay : PACK_PLAIN;
+  float* bias32 = nullptr;      // packed order for the MFMA kernels
+  float* bias_plain = nullptr;  // column order for the generic kernel
+  if (bias) {
+    bias32 = (float*)ws;
+    bias_plain = (float*)(ws + bias_bytes);
+    FL_CHECK_LAUNCH(launch_cast(bias, dtype, bias_plain, FL_F32, out_cols, 0, ctx->stream));
+    FL_CHECK_LAUNCH(launch_pack_vec_f32(bias_plain, out_cols, bias32, epi.layout, ctx->stream));
+  }
   epi.bias = bias32;
   const void* wnk = w;
-  bool mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, x, in_cols, y,
+  void* pk = ws + 2 * bias_bytes;
+  bool mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, pk, in_cols, y,
                                 out_cols, epi);
   if (mfma && w_layout == FL_W_IN_OUT) {
-    void* pk = ws + bias_bytes;
-    FL_CHECK_LAUNCH(launch_transpose(dtype, w, in_cols, out_cols, pk, 0, ctx->stream));
+    FL_CHECK_LAUNCH(launch_transpose(dtype, w, in_cols, out_cols, pk, epi.layout, ctx->stream));
+    wnk = pk;
+  } else if (mfma && epi.layout != PACK_PLAIN) {
+    FL_CHECK_LAUNCH(launch_pack_rows(dtype, w, in_cols, out_cols, in_cols, pk, epi.layout,
+                                     ctx->stream));
     wnk = pk;
   }
   if (mfma) mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, wnk, in_cols, y,
@@ -444,7 +475,7 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   } else {
     const int tb = w_layout == FL_W_OUT_IN;
     FL_CHECK_LAUNCH(launch_gemm_generic(dtype, 0, tb, rows, out_cols, in_cols, 1.0f, x, in_cols,
-                                        w, tb ? in_cols : out_cols, y, out_cols, bias32, epi_act,
+                                        w, tb ? in_cols : out_cols, y, out_cols, bias_plain, epi_act,
                                         math, ctx->stream));
   }
   if (act == FL_ACT_SWIGLU) {

@@ -99,8 +99,16 @@ __device__ inline float gelu_ref(float x) {
 
 __device__ inline float tanh_exact(float x) { return tanhf(x); }
 
+// tanh(y) = 1 - 2 / (exp(2y) + 1) on the hardware exp2 / reciprocal:
+// absolute error ~1e-7, which is what GELU's 0.5 x (1 + tanh) needs (the
+// stand-alone tanh activation keeps the libm function).
+__device__ inline float tanh_abs_fast(float y) {
+  const float e = __expf(2.0f * y);
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 __device__ inline float gelu_exact(float x) {
-  return 0.5f * x * (1.0f + tanh_exact(0.7978845608f * (x + 0.044715f * x * x * x)));
+  return 0.5f * x * (1.0f + tanh_abs_fast(0.7978845608f * (x + 0.044715f * x * x * x)));
 }
 
 template <int MATH> __device__ inline float gelu_m(float x) {
@@ -117,7 +125,8 @@ template <int MATH> __device__ inline float silu_m(float x) {
 #pragma clang fp contract(off)
     return x / (1.0f + (float)exp(-(double)x));
   } else {
-    return x / (1.0f + __expf(-x));
+    // Hardware reciprocal (1 ulp): exp(-x) = inf gives -0, exp(-x) = 0 gives x.
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
   }
 }
 

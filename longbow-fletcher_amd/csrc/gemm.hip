@@ -15,6 +15,21 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Ping-pong kernel (16-bit GEMMs with N % 256 == 0): K step, LDS stages and
+// row-block group of the tile order.
+#ifndef FL_GEMM_PP
+#define FL_GEMM_PP 1
+#endif
+#ifndef FL_GEMM_PP_BK
+#define FL_GEMM_PP_BK 32
+#endif
+#ifndef FL_GEMM_PP_NS
+#define FL_GEMM_PP_NS 4
+#endif
+#ifndef FL_GEMM_PP_GROUP_M
+#define FL_GEMM_PP_GROUP_M 8
+#endif
+
 namespace fl {
 
 template <typename T> struct Mfma;
@@ -699,13 +714,16 @@ __global__ void __launch_bounds__(WM* WN * 64, 2) gemm_lds32_kernel(GemmParams p
 // epilogue, so neither the prologue latency nor the epilogue stalls the
 // MFMA pipe.  BK = 32 (64-byte LDS rows, 4 chunks, swizzle (row >> 1) & 3).
 // ---------------------------------------------------------------------------
-template <typename T, int EPI, int MATH>
-__device__ inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[4][8], int m0,
+template <typename T, int EPI, int MATH, bool BIAS = true>
+__device__ __attribute__((always_inline)) inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[4][8], int m0,
                                      int nbase, int wm_off, int lane) {
   constexpr int TM = 8, FN = 4;
+  // Opaque copy of the lane id: stops lane-dependent epilogue addresses from
+  // being hoisted out of a persistent kernel's tile loop into registers.
+  asm volatile("" : "+v"(lane));
   T* C = (T*)p.C;
   const int lrow = lane & 15, lgrp = lane >> 4;
-  const float* bias = p.epi.bias;
+  const float* bias = BIAS ? p.epi.bias : nullptr;
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     const int m = m0 + wm_off + t * 16 + lrow;
@@ -717,11 +735,8 @@ __device__ inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[
         const int ng = nbase + 2 * j * 16 + lgrp * 4;
         float4_t gt = acc[2 * j][t], up = acc[2 * j + 1][t];
         if (bias) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            gt[i] += bias[ng + i];
-            up[i] += bias[ng + 16 + i];
-          }
+          gt += *(const float4_t*)(bias + ng);
+          up += *(const float4_t*)(bias + ng + 16);
         }
         float4_t o;
 #pragma unroll
@@ -734,10 +749,7 @@ __device__ inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         v[q] = acc[q][t];
-        if (bias) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[q][i] += bias[hb + q * 16 + lgrp * 4 + i];
-        }
+        if (bias) v[q] += *(const float4_t*)(bias + hb + q * 16 + lgrp * 4);
       }
       if (hb < p.epi.rope_cols) {
 #pragma clang fp contract(off)
@@ -760,13 +772,13 @@ __device__ inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[
       for (int f = 0; f < FN; ++f) {
         const int n = nbase + f * 16 + lgrp * 4;
         float4_t v = acc[f][t];
-        if (bias) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] += bias[n + i];
-        }
+        if (bias) v += *(const float4_t*)(bias + n);
         store4<T>(crow + n, act4<EPI, MATH>(v));
       }
     }
+    // One row block at a time: hoisting every block's table loads would
+    // need more registers than the accumulators leave.
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -887,6 +899,366 @@ __global__ void __launch_bounds__(256, 2) gemm_persist_kernel(GemmParams p, int 
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong epilogue.  B (and the bias) are packed so that the 16 values a
+// lane holds for one row block are adjacent outputs (PackLayout), so each
+// lane stores 16 bytes at a time.  The bias is read in packed order.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ inline void store8(T* dst, float4_t a, float4_t b) {
+  if constexpr (Elem<T>::dtype == F16) {
+    half8_t h = {(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+                 (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
+    *(half8_t*)dst = h;
+  } else {
+    bf16x8_t h = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                  (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
+    *(bf16x8_t*)dst = h;
+  }
+}
+
+template <typename T, int EPI, int MATH, bool BIAS>
+__device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmParams& p,
+                                                                  const float4_t (&acc)[4][8],
+                                                                  int m0, int nbase, int wm_off,
+                                                                  int lane) {
+  constexpr int TM = 8;
+  // Opaque copy of the lane id: stops lane-dependent epilogue addresses from
+  // being hoisted out of the tile loop into registers.
+  asm volatile("" : "+v"(lane));
+  T* C = (T*)p.C;
+  const int lrow = lane & 15, g = lane >> 4;
+  const float* bias = BIAS ? p.epi.bias : nullptr;
+  auto biased = [&](int f, int t) __attribute__((always_inline)) {
+    float4_t v = acc[f][t];
+    if (bias) v += *(const float4_t*)(bias + nbase + f * 16 + g * 4);
+    return v;
+  };
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    // Rows past M are computed on row M-1's inputs and not stored.
+    const int m = m0 + wm_off + t * 16 + lrow;
+    const bool ok = m < p.M;
+    const int mc = ok ? m : p.M - 1;
+    T* crow = C + (size_t)mc * p.ldc;
+    if constexpr (EPI == EPI_SWIGLU) {
+      // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
+      float4_t o[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4_t gt = biased(2 * h, t), up = biased(2 * h + 1, t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(gt[i]) * up[i];
+      }
+      if (ok) store8<T>(crow + nbase / 2 + g * 8, o[0], o[1]);
+    } else if constexpr (EPI == EPI_ROPE) {
+      // PACK_ROPE: tiles 0 / 1 hold dims 8g+i / 8g+4+i of the head, tiles
+      // 2 / 3 their rotate-half partners 32+8g+i / 32+8g+4+i.
+      float4_t v[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) v[f] = biased(f, t);
+      if (nbase < p.epi.rope_cols) {
+#pragma clang fp contract(off)
+        const float4_t* cs = (const float4_t*)(p.epi.rope_cs + (size_t)p.epi.pos[mc] * 32 + g * 8);
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4_t c = cs[f * 2 + h];  // (cos, sin) of dims 8g + 4f + 2h, +1
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int i = 2 * h + e;
+              const float x1 = v[f][i], x2 = v[f + 2][i];
+              const float co = c[2 * e], si = c[2 * e + 1];
+              v[f][i] = x1 * co - x2 * si;
+              v[f + 2][i] = x1 * si + x2 * co;
+            }
+          }
+        }
+      }
+      if (ok) {
+        store8<T>(crow + nbase + g * 8, v[0], v[1]);
+        store8<T>(crow + nbase + 32 + g * 8, v[2], v[3]);
+      }
+    } else {
+      // PACK_LANE16: tile f holds outputs 16g+4f+i.
+      float4_t v[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) v[f] = act4<EPI, MATH>(biased(f, t));
+      if (ok) {
+        store8<T>(crow + nbase + g * 16, v[0], v[1]);
+        store8<T>(crow + nbase + g * 16 + 8, v[2], v[3]);
+      }
+    }
+    // One row block at a time: hoisting every block's table loads would
+    // need more registers than the accumulators leave.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong 16-bit GEMM: 256x256 tiles, 8 waves in two groups of four (one
+// wave of each group per SIMD), NS LDS stages of BK-deep K slices, one
+// workgroup per CU walking its tiles as one continuous stream of K steps.
+//
+// Each K step takes two barrier-separated ticks per group: a memory tick
+// (run a pending epilogue, read this step's fragments from LDS into
+// registers, issue the DMA of step s+NS-1) and a compute tick (MFMAs on
+// registers only).  Group 1 runs one tick behind group 0, so on every SIMD
+// one wave issues MFMAs while the other does its memory work.
+//
+// Tick 2s: group 0 reads stage s%NS and issues its half of step s+NS-1 into
+// stage (s-1)%NS; group 1 computes step s-1.  Tick 2s+1: group 0 computes
+// step s; group 1 reads stage s%NS and issues its half of step s+NS-1.
+// Stage (s-1)%NS was last read in tick 2s-1.  At the end of tick 2s+1 each
+// wave waits until its own DMA of step s+1 has landed, so step s+1 is
+// complete in LDS when tick 2s+2 starts.
+//
+// Wave (g, w) owns output rows [128g, 128g+128) x features [64w, 64w+64):
+// the same 128x64 wave tile and epilogue as the 4-wave kernels.  Group 0
+// loads the activation rows, group 1 the weight rows.
+// ---------------------------------------------------------------------------
+__device__ inline void pp_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// 16-byte chunk swizzle of an LDS row: the 16 rows of one fragment read
+// land on distinct banks (64-byte rows: pairs of rows share a 128-byte bank
+// line; 128-byte rows: one row per bank line).
+template <int CPR>
+__device__ inline int pp_swz(int row) {
+  if constexpr (CPR == 4) return (row >> 1) & 3;
+  else return (row & 7) ^ ((row >> 3) & 1);
+}
+
+template <typename T, int EPI, int MATH, int BK, int NS>
+__global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int ROWB = BK * 2;                 // bytes per LDS row
+  constexpr int CPR = BK / 8;                  // 16-byte chunks per row
+  constexpr int RPL = 64 / CPR;                // rows per 1 KB DMA load
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int KS = BK / 32;                  // MFMA k steps per K step
+  constexpr int TM = 8, FN = 4, WTM = 128, WTN = 64;
+  constexpr int NLD = STAGE / 1024 / 8;        // 1 KB DMA loads per wave per step
+  constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
+  static_assert(BK == 32 || BK == 64, "BK 32 or 64");
+  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS stages");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wn = wave & 3;
+
+  // Persistent tile order: when the tiles split evenly, the workgroups of one
+  // XCD take consecutive runs of the grouped order, so the tiles an XCD has
+  // in flight share activation row-blocks and weight column-blocks in L2.
+  const int G = (int)gridDim.x;
+  const int me = xcd_remap((int)blockIdx.x, G);
+  const int my_tiles = me < ntiles ? (ntiles - 1 - me) / G + 1 : 0;
+  if (my_tiles == 0) return;
+  const bool chunked = (ntiles % G == 0) && (G % 8 == 0);
+  const int per = G / 8;
+  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
+  const int per_group = GROUP_M * num_n;
+  auto coords = [&](int i, int& m0, int& n0) __attribute__((always_inline)) {
+    const int L = chunked ? (me / per) * (my_tiles * per) + i * per + (me % per) : i * G + me;
+    const int g = L / per_group;
+    const int first_m = g * GROUP_M;
+    const int gsize = min(num_m - first_m, GROUP_M);
+    const int r = L - g * per_group;
+    m0 = (first_m + r % gsize) * BM;
+    n0 = (r / gsize) * BN;
+  };
+  const int nk = p.K / BK;
+  const int total = my_tiles * nk;
+
+  // DMA geometry: wave (g, w) fills rows [RPL*NLD*w, RPL*NLD*(w+1)) of the
+  // activation (g = 0) or weight (g = 1) half of a stage; lane l writes
+  // 16-byte chunk l%CPR of row l/CPR of each 1 KB load, holding global chunk
+  // (l%CPR) ^ swz(row).  Activation rows past M re-read row M-1 (never
+  // stored).
+  const char* gsrc = grp == 0 ? (const char*)p.A : (const char*)p.B;
+  const int ld = grp == 0 ? p.lda : p.ldb;
+  const int lrow = lane / CPR, lcol = lane % CPR;
+  uint32_t off[NLD];
+  const char* gbase = nullptr;
+  auto load_tile = [&](int ti) __attribute__((always_inline)) {
+    int m0, n0;
+    coords(ti, m0, n0);
+    const int r0 = grp == 0 ? m0 : n0;
+    const int lim = grp == 0 ? p.M - 1 - m0 : BN - 1;
+    gbase = gsrc + (size_t)r0 * ld * sizeof(T);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int row = (wn * NLD + j) * RPL + lrow;
+      const int c = lcol ^ pp_swz<CPR>(row);
+      off[j] = (uint32_t)(min(row, lim) * ld + c * 8) * (uint32_t)sizeof(T);
+    }
+  };
+  // DMA cursor: the step that the next issue loads.  Past the last step it
+  // keeps re-loading slice 0 of the last tile (in bounds, into a stage that
+  // is never read again), so every tick issues the same number of loads and
+  // the wait counts stay uniform.
+  int ld_tile = 0, ld_k = 0;
+  auto issue_one = [&](char* stage, int j) __attribute__((always_inline)) {
+    const char* src = gbase + (size_t)ld_k * BK * sizeof(T);
+    char* dst = stage + grp * (BM * ROWB) + wn * NLD * 1024;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + off[j]),
+                                     (__attribute__((address_space(3))) void*)(dst + j * 1024), 16,
+                                     0, 0);
+  };
+  auto advance = [&]() __attribute__((always_inline)) {
+    if (++ld_k == nk) {
+      ld_k = 0;
+      if (ld_tile + 1 < my_tiles) load_tile(++ld_tile);
+    }
+  };
+  auto issue = [&](char* stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) issue_one(stage, j);
+    advance();
+  };
+
+  // Fragment reads: row base + (lane & 15), k chunk 4*ks + (lane >> 4).
+  const int fr = lane & 15, fg = lane >> 4;
+  const int swz = pp_swz<CPR>(fr);
+  const int a_row0 = (grp * WTM + fr) * ROWB;
+  const int b_row0 = BM * ROWB + (wn * WTN + fr) * ROWB;
+  u32x4_t fa[KS][TM], fb[KS][FN];
+  auto read_frags = [&](const char* st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int co = ((ks * 4 + fg) ^ swz) << 4;
+#pragma unroll
+      for (int t = 0; t < TM; ++t) fa[ks][t] = *(const u32x4_t*)(st + a_row0 + t * 16 * ROWB + co);
+#pragma unroll
+      for (int f = 0; f < FN; ++f) fb[ks][f] = *(const u32x4_t*)(st + b_row0 + f * 16 * ROWB + co);
+    }
+  };
+
+  float4_t acc[FN][TM];
+  // The first K step of a tile multiplies into zero instead of clearing the
+  // accumulators after each epilogue.
+  // Compute tick: the step's MFMAs, with this wave's DMA of step s+NS-1
+  // (into `stage`) issued one load per MFMA group, so the DMA queue fills
+  // gradually instead of in one burst.
+  constexpr int NMF = KS * FN * TM;
+  constexpr int PER = NMF / NLD;
+  static_assert(NMF % NLD == 0, "loads spread evenly over the MFMAs");
+  auto compute = [&](char* stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+          Mfma<T>::mma(acc[f][t], fb[ks][f], fa[ks][t]);
+          const int i = (ks * FN + f) * TM + t;
+          if (i % PER == PER - 1) issue_one(stage, i / PER);
+        }
+    // Interleave PER MFMAs and one DMA load (the RoPE variant leaves the
+    // order to the scheduler: pinning it there costs registers it lacks).
+    if constexpr (EPI != EPI_ROPE) {
+#pragma unroll
+      for (int g = 0; g < NLD; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+    }
+    advance();
+  };
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int f = 0; f < FN; ++f)
+#pragma unroll
+      for (int t = 0; t < TM; ++t) acc[f][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  auto epilogue = [&](int ti) __attribute__((always_inline)) {
+    int m0, n0;
+    coords(ti, m0, n0);
+    pp_epilogue<T, EPI, MATH, EPI != EPI_ROPE>(p, acc, m0, n0 + wn * WTN, grp * WTM, lane);
+    zero_acc();
+    // Keep the next fragment reads (and their registers) after the epilogue.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: steps 0 .. NS-2 into stages 0 .. NS-2.
+  zero_acc();
+  load_tile(0);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(lds + s * STAGE);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  pp_barrier();
+
+  // DMA wait for step s+1: the loads of one wave complete in issue order and
+  // every tick issues NLD of them, so "step s+1 landed" is "at most the
+  // loads of the NS-2 later steps outstanding".  Epilogue stores also count
+  // in vmcnt; they can only make the wait longer, never shorter.
+  auto wait_next = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD * (NS - 2)) : "memory");
+  };
+
+  int ck = 0, ctile = 0;       // K step / tile of the next compute
+  bool pending = false;        // accumulators hold a finished tile
+  int ptile = 0;
+  if (grp == 0) {
+    for (int s = 0; s < total; ++s) {
+      // tick 2s: memory tick of step s
+      if (pending) {
+        epilogue(ptile);
+        pending = false;
+      }
+      read_frags(lds + (s % NS) * STAGE);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      pp_barrier();
+      // tick 2s+1: compute step s, DMA of step s+NS-1
+      compute(lds + ((s + NS - 1) % NS) * STAGE);
+      if (++ck == nk) {
+        ck = 0;
+        pending = true;
+        ptile = ctile++;
+      }
+      wait_next();
+      pp_barrier();
+    }
+  } else {
+    for (int s = 0; s < total; ++s) {
+      // tick 2s: compute step s-1, DMA of step s+NS-1
+      char* nxt = lds + ((s + NS - 1) % NS) * STAGE;
+      if (s > 0) {
+        compute(nxt);
+        if (++ck == nk) {
+          ck = 0;
+          pending = true;
+          ptile = ctile++;
+        }
+      } else {
+        issue(nxt);
+      }
+      pp_barrier();
+      // tick 2s+1: memory tick of step s.  With an epilogue, wait for the
+      // DMA first so the wait does not include the new stores.
+      if (pending) {
+        wait_next();
+        epilogue(ptile);
+        pending = false;
+        read_frags(lds + (s % NS) * STAGE);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      } else {
+        read_frags(lds + (s % NS) * STAGE);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_next();
+      }
+      pp_barrier();
+    }
+    compute(lds + ((total + NS - 1) % NS) * STAGE);  // its DMA is a dummy reload
+    pending = true;
+    ptile = ctile;
+  }
+  if (pending) epilogue(ptile);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
 // Tile configurations.  16-bit: 256x256 tiles of 4 waves x (128x128) when
 // N % 256 == 0 (4 MFMAs per 16-byte LDS fragment read, 144 KB of LDS double
 // buffered, one workgroup per CU), else 256x128 tiles of 4 x (128x64).
@@ -952,6 +1324,22 @@ static hipError_t launch_persist(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Epilogues the ping-pong kernel is built for.  The others (GELU, tanh, the
+// reference-formula SiLU) need more registers than it leaves next to its
+// accumulators and take the 4-wave kernels; so does RoPE with a bias.
+constexpr bool pp_epilogue_ok(int epi, int math) {
+  return epi == EPI_STORE || epi == EPI_ROPE || (math == MATH_EXACT && epi == EPI_SWIGLU);
+}
+
+template <typename T, int EPI, int MATH>
+static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
+  const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
+  const int grid = std::min(ntiles, cu_count());
+  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, FL_GEMM_PP_BK, FL_GEMM_PP_NS>), dim3(grid), dim3(512),
+                     0, s, p, ntiles);
+  return hipGetLastError();
+}
+
 template <typename T, typename C, int EPI, int MATH>
 static hipError_t launch_lds32(const GemmParams& p, hipStream_t s) {
   const int num_m = (p.M + C::BM - 1) / C::BM;
@@ -978,6 +1366,12 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
   if constexpr (sizeof(T) == 4) {
     return launch_cfg<T, CfgF32, EPI, MATH>(p, s);
   } else {
+    // B packed for the ping-pong kernel (gemm_pp_layout) goes there; only the
+    // epilogues it was built for reach this point with such a layout.
+    if (p.epi.layout >= PACK_LANE16) {
+      if constexpr (pp_epilogue_ok(EPI, MATH)) return launch_pp<T, EPI, MATH>(p, s);
+      return hipErrorInvalidValue;
+    }
 #if FL_GEMM_MFMA32 == 1
     if (p.K % (2 * FL_GEMM_BK) == 0) return launch_lds32<T, Cfg256x128, EPI, MATH>(p, s);
 #elif FL_GEMM_MFMA32 == 2
@@ -1023,9 +1417,26 @@ static bool cfg_ok(int N, int K) {
   else return N % Cfg256x128::BN == 0 && K % Cfg256x128::BK == 0;
 }
 
+int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
+  if (!FL_GEMM_PP || (dtype != F16 && dtype != BF16)) return -1;
+  if (N <= 0 || K <= 0 || N % 256 || K % FL_GEMM_PP_BK) return -1;
+  if (!pp_epilogue_ok(epi_kind, math)) return -1;
+  if (epi_kind == EPI_ROPE) return has_bias ? -1 : PACK_ROPE;
+  return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
+}
+
 bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
                        int ldb, const void* C, int ldc, const GemmEpilogue& epi) {
   if (M <= 0 || N <= 0 || K <= 0) return false;
+  if (epi.layout >= PACK_LANE16) {
+    if (gemm_pp_layout(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr) != epi.layout)
+      return false;
+    if (lda % 8 || ldb % 8 || ldc % 8) return false;
+    if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C | (uintptr_t)epi.bias) & 15) return false;
+    if (epi.kind == EPI_ROPE && (epi.rope_cols % 64 || !epi.pos || !epi.rope_cs)) return false;
+    return true;
+  }
+  if (epi.layout != (epi.kind == EPI_SWIGLU ? PACK_SWIGLU16 : PACK_PLAIN)) return false;
   const int esz = dtype == F32 ? 4 : 2;
   const int epc = 16 / esz;
   bool shape = dtype == F32 ? cfg_ok<float>(N, K)
@@ -1034,6 +1445,7 @@ bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, c
   if (lda % epc || ldb % epc || ldc % 4) return false;
   if (((uintptr_t)A | (uintptr_t)B) & 15) return false;
   if ((uintptr_t)C & (4 * esz - 1)) return false;
+  if ((uintptr_t)epi.bias & 15) return false;
   if (epi.kind == EPI_SWIGLU && (N % 32)) return false;
   if (epi.kind == EPI_ROPE && (epi.rope_cols % 64 || !epi.pos || !epi.rope_cs)) return false;
   return true;
@@ -1126,7 +1538,7 @@ hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N
 // output columns are reordered into 16-column blocks g0 u0 g1 u1 ...
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int swiglu) {
+__global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int layout) {
   __shared__ T tile[32][33];
   const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
@@ -1135,32 +1547,56 @@ __global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int sw
     if (r < rows && c < cols) tile[j][tx] = in[(size_t)r * cols + c];
   }
   __syncthreads();
-  const int half = cols / 2;
   for (int j = ty; j < 32; j += 8) {
     const int n = bx + j, k = by + tx;  // output row n (input column), column k
-    if (n < cols && k < rows) {
-      int pn = n;
-      if (swiglu) pn = n < half ? (n / 16) * 32 + (n % 16) : ((n - half) / 16) * 32 + 16 + (n - half) % 16;
-      out[(size_t)pn * rows + k] = tile[tx][j];
-    }
+    if (n < cols && k < rows) out[(size_t)packed_row(n, cols, layout) * rows + k] = tile[tx][j];
   }
 }
 
+// out[packed_row(n), :] = in[n, :], one row per block of 64 threads x 16 B.
+__global__ void pack_rows_kernel(const char* in, size_t ld_bytes, int N, size_t row_bytes,
+                                 char* out, int layout) {
+  const int n = blockIdx.x;
+  const char* src = in + (size_t)n * ld_bytes;
+  char* dst = out + (size_t)packed_row(n, N, layout) * row_bytes;
+  for (size_t b = (size_t)threadIdx.x * 16; b < row_bytes; b += 64 * 16)
+    *(u32x4_t*)(dst + b) = *(const u32x4_t*)(src + b);
+}
+
+__global__ void pack_vec_kernel(const float* in, int N, float* out, int layout) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < N) out[packed_row(n, N, layout)] = in[n];
+}
+
+hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, void* out,
+                            int layout, hipStream_t s) {
+  const size_t esz = dtype == F32 ? 4 : 2;
+  if (((uintptr_t)in | (uintptr_t)out | (ld * esz) | (K * esz)) & 15) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(N), dim3(64), 0, s, (const char*)in, ld * esz, N,
+                     K * esz, (char*)out, layout);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t s) {
+  hipLaunchKernelGGL(pack_vec_kernel, dim3((N + 255) / 256), dim3(256), 0, s, in, N, out, layout);
+  return hipGetLastError();
+}
+
 hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
-                            int swiglu_interleave, hipStream_t s) {
+                            int layout, hipStream_t s) {
   dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(256);
   switch (dtype) {
     case F32:
       hipLaunchKernelGGL(transpose_kernel<float>, grid, block, 0, s, (const float*)in, rows, cols,
-                         (float*)out, swiglu_interleave);
+                         (float*)out, layout);
       break;
     case F16:
       hipLaunchKernelGGL(transpose_kernel<_Float16>, grid, block, 0, s, (const _Float16*)in,
-                         rows, cols, (_Float16*)out, swiglu_interleave);
+                         rows, cols, (_Float16*)out, layout);
       break;
     case BF16:
       hipLaunchKernelGGL(transpose_kernel<__bf16>, grid, block, 0, s, (const __bf16*)in, rows,
-                         cols, (__bf16*)out, swiglu_interleave);
+                         cols, (__bf16*)out, layout);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -15,17 +15,65 @@ enum EpiKind : int {
   EPI_ROPE = 4,    // rotate-half RoPE on columns [0, rope_cols), head_dim 64
 };
 
+// Row order of a packed [N, K] weight matrix (and of its fp32 bias): which
+// packed row holds logical output column n.  Within each 64-row block the
+// ping-pong layouts put the columns an MFMA lane accumulates (4 rows of each
+// of 4 16-row tiles) on adjacent outputs, so the epilogue stores 16 bytes per
+// lane:
+//   PACK_LANE16       lane g holds outputs [16g, 16g+16) of the block
+//   PACK_ROPE         lane g holds [8g, 8g+8) and [32+8g, 32+8g+8) of a
+//                     64-wide head, i.e. both halves of its rotate-half pairs
+//   PACK_SWIGLU_LANE  lane g holds gate and up of outputs [8g, 8g+8) of the
+//                     block's 32 outputs (gate = column o, up = column N/2+o)
+// PACK_SWIGLU16 is the 4-wave kernels' gate/up interleave in 16-row blocks.
+enum PackLayout : int {
+  PACK_PLAIN = 0,
+  PACK_SWIGLU16 = 1,
+  PACK_LANE16 = 2,
+  PACK_ROPE = 3,
+  PACK_SWIGLU_LANE = 4,
+};
+__host__ __device__ inline int packed_row(int n, int N, int layout) {
+  switch (layout) {
+    case PACK_SWIGLU16: {
+      const int half = N / 2;
+      return n < half ? (n / 16) * 32 + n % 16 : ((n - half) / 16) * 32 + 16 + (n - half) % 16;
+    }
+    case PACK_LANE16: {
+      const int r = n % 64, g = r / 16, f = (r / 4) % 4, i = r % 4;
+      return n - r + f * 16 + g * 4 + i;
+    }
+    case PACK_ROPE: {
+      const int r = n % 64, r2 = r % 32, g = r2 / 8, f = (r2 / 4) % 2 + 2 * (r / 32), i = r % 4;
+      return n - r + f * 16 + g * 4 + i;
+    }
+    case PACK_SWIGLU_LANE: {
+      const int half = N / 2, up = n >= half, o = up ? n - half : n;
+      const int ro = o % 32, g = ro / 8, f = 2 * ((ro / 4) % 2) + up, i = ro % 4;
+      return (o / 32) * 64 + f * 16 + g * 4 + i;
+    }
+    default: return n;
+  }
+}
+
 struct GemmEpilogue {
   int kind = EPI_STORE;
   int math = 0;                    // MathMode for GELU / tanh / silu
-  const float* bias = nullptr;     // fp32 [N] (packed order) or null
+  const float* bias = nullptr;     // fp32 [N] in packed row order, or null
   const float2* rope_cs = nullptr; // [max_pos][32] (cos, sin)
   const int* pos = nullptr;        // [M] position of each row in its sequence
   int rope_cols = 0;
+  int layout = PACK_PLAIN;         // PackLayout of B and bias
 };
 
+// The packing the ping-pong GEMM needs for this problem, or -1 when that
+// kernel does not take it (the caller then packs PACK_PLAIN / PACK_SWIGLU16
+// for the 4-wave kernels).
+int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias);
+
 // C[M, N] = A[M, K] * B[N, K]^T with the epilogue.  MFMA path; requires
-// N % 64 == 0, K % 64 (16-bit) or K % 32 (fp32) == 0 and 16-byte aligned rows.
+// N % 64 == 0, K % 64 (16-bit) or K % 32 (fp32) == 0 and 16-byte aligned rows,
+// and B packed as epi.layout says.
 bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
                        int ldb, const void* C, int ldc, const GemmEpilogue& epi);
 hipError_t launch_gemm_nt(int dtype, const void* A, int lda, const void* B, int ldb, void* C,
@@ -38,10 +86,15 @@ hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N
                                void* C, int ldc, const float* bias, int act, int math,
                                hipStream_t stream);
 
-// out[n, k] = in[k, n] (dtype elements), optionally interleaving SwiGLU
-// gate/up halves in 16-row blocks.
+// out[packed_row(n), k] = in[k, n] (dtype elements): [rows = K, cols = N] to
+// a packed [N, K] weight matrix.
 hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
-                            int swiglu_interleave, hipStream_t stream);
+                            int layout, hipStream_t stream);
+// out[packed_row(n), :] = in[n, :] for an [N, K] matrix with row stride ld.
+hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, void* out,
+                            int layout, hipStream_t stream);
+// out[packed_row(n)] = in[n] for an fp32 vector of N.
+hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t stream);
 
 // ---- attention ------------------------------------------------------------
 struct AttnWork {

@@ -54,6 +54,8 @@ struct fl_model {
   bool swiglu = false, rope = false;
   bool mfma_qkv = false, mfma_o = false, mfma_up = false, mfma_down = false;
   bool rope_fused = false;
+  // PackLayout of each projection's packed weights and bias.
+  int lay_qkv = PACK_PLAIN, lay_o = PACK_PLAIN, lay_up = PACK_PLAIN, lay_down = PACK_PLAIN;
 
   void* word = nullptr;
   void* pos = nullptr;
@@ -330,6 +332,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       ProfScope ps(m, P_QKV);
       GemmEpilogue e;
       e.bias = w.bqkv;
+      e.layout = m->lay_qkv;
       if (m->rope && m->rope_fused) {
         e.kind = EPI_ROPE;
         e.rope_cs = m->rope_cs;
@@ -361,6 +364,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       ProfScope ps(m, P_O);
       GemmEpilogue e;
       e.bias = w.bo;
+      e.layout = m->lay_o;
       M_ST(gemm(m, m->mfma_o, m->CTX, w.wo, m->TMP, Ti, H, H, e));
     }
     {
@@ -372,6 +376,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       GemmEpilogue e;
       e.bias = w.bi;
       e.math = m->cfg.math;
+      e.layout = m->lay_up;
       if (m->swiglu) {
         if (m->mfma_up) {
           e.kind = EPI_SWIGLU;
@@ -390,6 +395,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       ProfScope ps(m, P_DOWN);
       GemmEpilogue e;
       e.bias = w.bd;
+      e.layout = m->lay_down;
       M_ST(gemm(m, m->mfma_down, m->QKV, w.wd, m->TMP, Ti, H, m->I, e));
     }
     {
@@ -453,6 +459,21 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
   m->mfma_up = mfma_shape_ok(m->dtype, m->Ni, m->H) && (!m->swiglu || m->I % 16 == 0);
   m->mfma_down = mfma_shape_ok(m->dtype, m->H, m->I);
   m->rope_fused = m->mfma_qkv && m->hd == 64;
+  {
+    const bool has_bias = c.has_bias != 0;
+    auto pick = [&](bool mfma, int N, int K, int kind, int fallback) {
+      if (!mfma) return (int)PACK_PLAIN;
+      const int l = gemm_pp_layout(m->dtype, N, K, kind, c.math, has_bias);
+      return l >= 0 ? l : fallback;
+    };
+    m->lay_qkv = pick(m->mfma_qkv, 3 * m->H, m->H, m->rope && m->rope_fused ? EPI_ROPE : EPI_STORE,
+                      PACK_PLAIN);
+    m->lay_o = pick(m->mfma_o, m->H, m->H, EPI_STORE, PACK_PLAIN);
+    m->lay_up = m->swiglu ? pick(m->mfma_up, m->Ni, m->H, EPI_SWIGLU, PACK_SWIGLU16)
+                          : pick(m->mfma_up, m->Ni, m->H, EPI_GELU, PACK_PLAIN);
+    if (m->swiglu && !m->mfma_up) m->lay_up = PACK_PLAIN;
+    m->lay_down = pick(m->mfma_down, m->H, m->I, EPI_STORE, PACK_PLAIN);
+  }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
     void* p;
@@ -554,9 +575,14 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
     return FL_OK;
   };
   // [in, out] reference matrix -> [out, in] packed (optionally SwiGLU interleaved)
-  auto pack = [&](void* dst, int rows, int cols, int inter) -> int {
+  auto pack = [&](void* dst, int rows, int cols, int layout) -> int {
     M_CHECK(launch_cast(f32, FL_F32, cvt, dt, n, 0, s));
-    M_CHECK(launch_transpose(dt, cvt, rows, cols, dst, inter, s));
+    M_CHECK(launch_transpose(dt, cvt, rows, cols, dst, layout, s));
+    return FL_OK;
+  };
+  // fp32 bias vector in the packed row order of its weights.
+  auto pack_bias = [&](float* dst, int N, int layout) -> int {
+    M_CHECK(launch_pack_vec_f32(f32, N, dst, layout, s));
     return FL_OK;
   };
   if (!per_layer) {
@@ -577,33 +603,24 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
     if (field == "q_w" || field == "k_w" || field == "v_w") {
       M_ST(expect(H * H));
       const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
-      M_ST(pack((char*)L.wqkv + (size_t)part * H * H * esz, (int)H, (int)H, 0));
+      // The packed orders permute within 64-row blocks, so each part packs alone.
+      M_ST(pack((char*)L.wqkv + (size_t)part * H * H * esz, (int)H, (int)H, m->lay_qkv));
     } else if (field == "q_b" || field == "k_b" || field == "v_b") {
       M_ST(expect(H));
       const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
-      M_ST(copy_f32(L.bqkv + part * H));
-    } else if (field == "o_w") { M_ST(expect(H * H)); M_ST(pack(L.wo, (int)H, (int)H, 0)); }
-    else if (field == "o_b") { M_ST(expect(H)); M_ST(copy_f32(L.bo)); }
+      M_ST(pack_bias(L.bqkv + part * H, (int)H, m->lay_qkv));
+    } else if (field == "o_w") { M_ST(expect(H * H)); M_ST(pack(L.wo, (int)H, (int)H, m->lay_o)); }
+    else if (field == "o_b") { M_ST(expect(H)); M_ST(pack_bias(L.bo, (int)H, m->lay_o)); }
     else if (field == "attn_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_g)); }
     else if (field == "attn_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_b)); }
     else if (field == "inter_w") {
       M_ST(expect(H * Ni));
-      M_ST(pack(L.wi, (int)H, (int)Ni, m->swiglu && m->mfma_up));
+      M_ST(pack(L.wi, (int)H, (int)Ni, m->lay_up));
     } else if (field == "inter_b") {
       M_ST(expect(Ni));
-      if (m->swiglu && m->mfma_up) {
-        std::vector<float> perm(Ni);
-        for (int64_t j = 0; j < Ni; ++j) {
-          const int64_t p = j < I ? (j / 16) * 32 + j % 16 : ((j - I) / 16) * 32 + 16 + (j - I) % 16;
-          perm[p] = data[j];
-        }
-        M_CHECK(hipMemcpyAsync(L.bi, perm.data(), Ni * 4, hipMemcpyHostToDevice, s));
-        M_CHECK(hipStreamSynchronize(s));
-      } else {
-        M_ST(copy_f32(L.bi));
-      }
-    } else if (field == "out_w") { M_ST(expect(I * H)); M_ST(pack(L.wd, (int)I, (int)H, 0)); }
-    else if (field == "out_b") { M_ST(expect(H)); M_ST(copy_f32(L.bd)); }
+      M_ST(pack_bias(L.bi, (int)Ni, m->lay_up));
+    } else if (field == "out_w") { M_ST(expect(I * H)); M_ST(pack(L.wd, (int)I, (int)H, m->lay_down)); }
+    else if (field == "out_b") { M_ST(expect(H)); M_ST(pack_bias(L.bd, (int)H, m->lay_down)); }
     else if (field == "out_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_g)); }
     else if (field == "out_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_b)); }
     else return fail(FL_ERR_INVALID, "unknown weight " + nm);

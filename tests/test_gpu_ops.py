@@ -111,6 +111,75 @@ def test_gemm_16bit(ctx, fl, orc, dtype, m, k, n):
     close(got, want, 2 * ulp * np.abs(want).max() + 1e-3, 2 * ulp)
 
 
+@pytest.mark.parametrize("m,k,n", [(65536, 768, 2304),   # 9 tiles per workgroup, XCD-chunked order
+                                   (65636, 768, 768),    # ragged last row block, uneven tile split
+                                   (32768, 3072, 768)])  # long K stream, 1-2 tiles per workgroup
+def test_gemm_16bit_many_tiles(ctx, fl, m, k, n):
+    # Rows checked: a sample spread over every row block plus the last rows.
+    rng = np.random.default_rng(m + k + n)
+    a = (rng.standard_normal((m, k)) * 0.5).astype(np.float32)
+    b = (rng.standard_normal((k, n)) * 0.05).astype(np.float32)
+    da, db = ctx.tensor(a, fl.F16), ctx.tensor(b, fl.F16)
+    got = ctx.gemm(da, db).numpy()
+    ar, br = f16(a), f16(b)
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), np.arange(m - 40, m)]))
+    want = ar[rows].astype(np.float64) @ br.astype(np.float64)
+    ulp = 2 ** -10
+    close(got[rows], want, 2 * ulp * np.abs(want).max() + 1e-3, 2 * ulp)
+
+
+def exact_activation(orc, x, w, b, act):
+    """FL_MATH_EXACT reference: the oracle's product, then the activation in
+    float64 (the oracle's own GELU is the reference's TanhFast formula, which
+    is up to 0.022 from tanh, simd.go)."""
+    y = orc.linear(x, w, b).astype(np.float64)
+    if act == 1:
+        return 0.5 * y * (1 + np.tanh(0.7978845608 * (y + 0.044715 * y ** 3)))
+    if act == 4:
+        h = y.shape[1] // 2
+        return y[:, :h] / (1 + np.exp(-y[:, :h])) * y[:, h:]
+    return y
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_gemm_16bit_transposed_b(ctx, fl, orc, dtype):
+    # B handed over as [n x k] (Tensor.T() of a weight): repacked by rows.
+    dt = fl.F16 if dtype == "f16" else fl.BF16
+    m, k, n = 700, 768, 1280
+    a, bt = rand(m, k), rand(n, k, scale=0.05)
+    da, dbt = ctx.tensor(a, dt), ctx.tensor(bt, dt)
+    got = ctx.gemm(da, dbt, trans_b=True).numpy()
+    want = orc.mul(da.numpy(), np.ascontiguousarray(dbt.numpy().T))
+    ulp = 2 ** -10 if dt == fl.F16 else 2 ** -7
+    close(got, want, 2 * ulp * np.abs(want).max() + 1e-3, 2 * ulp)
+
+
+@pytest.mark.parametrize("act", ["identity", "gelu"])
+def test_linear_16bit_out_in_bias(ctx, fl, orc, act):
+    a_id = {"identity": 0, "gelu": 1}[act]
+    x, w, b = rand(333, 512), rand(512, 768, scale=0.05), rand(768, scale=0.1)
+    dx, db = ctx.tensor(x, fl.F16), ctx.tensor(b, fl.F16)
+    dwt = ctx.tensor(np.ascontiguousarray(w.T), fl.F16)
+    got = ctx.linear(dx, dwt, db, act=a_id, math=fl.MATH_EXACT, w_layout=fl.W_OUT_IN).numpy()
+    want = exact_activation(orc, dx.numpy(), np.ascontiguousarray(dwt.numpy().T), db.numpy(), a_id)
+    ulp = 2 ** -10
+    close(got, want, 4 * ulp * np.abs(want).max() + 1e-3, 4 * ulp)
+
+
+@pytest.mark.parametrize("act", ["gelu", "swiglu", "identity"])
+def test_linear_16bit_fused_epilogues(ctx, fl, orc, act):
+    # Bias + activation fused into the 16-bit GEMM epilogue (bert.go:770-824
+    # FFN shapes), fast math, against the oracle on the rounded operands.
+    a_id = {"identity": 0, "gelu": 1, "swiglu": 4}[act]
+    m, k, n = 1100, 768, (6144 if act == "swiglu" else 3072)
+    x, w, b = rand(m, k), rand(k, n, scale=0.05), rand(n, scale=0.1)
+    dx, dw, db = ctx.tensor(x, fl.F16), ctx.tensor(w, fl.F16), ctx.tensor(b, fl.F16)
+    got = ctx.linear(dx, dw, db, act=a_id, math=fl.MATH_EXACT).numpy()
+    want = exact_activation(orc, dx.numpy(), dw.numpy(), db.numpy(), a_id)
+    ulp = 2 ** -10
+    close(got, want, 4 * ulp * np.abs(want).max() + 1e-3, 4 * ulp)
+
+
 @pytest.mark.parametrize("act", ["identity", "gelu", "tanh", "softmax", "swiglu"])
 def test_linear_f32_reference_math(ctx, fl, orc, act):
     a_id = {"identity": 0, "gelu": 1, "tanh": 2, "softmax": 3, "swiglu": 4}[act]
