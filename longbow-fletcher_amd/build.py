@@ -34,7 +34,8 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object
 # Per-file flags.  gemm.hip: keep MFMA accumulators in architectural VGPRs
 # (the accumulator-register form made the allocator copy accumulators every
 # K step).
-PER_FILE = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+PER_FILE = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+            "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _compile(src: pathlib.Path) -> pathlib.Path:

@@ -8,10 +8,13 @@
 //
 // Flash kernel (16-bit, exact math): computed transposed, S^T = K Q^T and
 // O^T = V^T P^T, so the probabilities leave the first MFMA already in the
-// operand layout of the second one (no cross-lane shuffle of P); only V is
-// transposed, once, while staging it into LDS.  A query column's 64 scores
-// of a key tile live in the 4 lanes {q, q+16, q+32, q+48}, so the row max
-// is a 2-step shuffle.
+// operand layout of the second one (no cross-lane shuffle of P).  K and V
+// tiles go global -> LDS by DMA, row-major with an XOR chunk swizzle; the
+// V^T operand is read with the gfx950 transposing LDS load.  A query
+// column's scores of a key tile live in the 4 lanes {q, q+16, q+32, q+48};
+// its row max is two permlane swaps and its row sum comes out of an extra
+// MFMA against a ones operand, so the softmax costs one FMA, one exp2, half
+// a max and half a pack per score.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -31,49 +34,73 @@ struct AttnParams {
 
 template <typename T> struct AttnMfma;
 template <> struct AttnMfma<_Float16> {
+  static constexpr uint32_t kOnes = 0x3C003C00u;  // two fp16 1.0
   __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
                                                __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float a, float b) {
-    _Float16 h[2] = {(_Float16)a, (_Float16)b};
-    uint32_t r;
-    __builtin_memcpy(&r, h, 4);
-    return r;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = {(_Float16)a, (_Float16)b};  // v_cvt_pk_f16_f32 (RNE)
+    return __builtin_bit_cast(uint32_t, h);
   }
 };
 template <> struct AttnMfma<__bf16> {
+  static constexpr uint32_t kOnes = 0x3F803F80u;  // two bf16 1.0
   __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float a, float b) {
-    __bf16 h[2] = {(__bf16)a, (__bf16)b};
-    uint32_t r;
-    __builtin_memcpy(&r, h, 4);
-    return r;
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 h = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32 (RNE)
+    return __builtin_bit_cast(uint32_t, h);
   }
 };
 
-// One workgroup = WAVES waves x 32 query rows of one (sequence, head);
-// key/value tiles of 64 rows are double-buffered through LDS.
+typedef short attn_s4 __attribute__((__vector_size__(8)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane block,
+// lane i receives element i%4 of the 8-byte rows addressed by lanes
+// i/4 + 4j, j = 0..3.
+__device__ inline u32x2_t lds_read_tr16(const lds_char* p) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                         (__attribute__((address_space(3))) attn_s4*)p));
+}
+
+// Max over the lanes {l, l^16, l^32, l^48} (v_permlane16/32_swap: each swap
+// returns the value pair of a lane and its xor-16 / xor-32 partner).
+__device__ inline float quad_max(float v) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  const uint32_t y = __builtin_bit_cast(uint32_t, v);
+  const auto b = __builtin_amdgcn_permlane32_swap(y, y, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+
+// One workgroup = WAVES waves x 32 query rows of one (sequence, head); key /
+// value tiles of 64 rows are double-buffered in LDS.  A tile is 64 rows of
+// 128 bytes; 16-byte chunk c of row r sits at chunk c ^ (r & 7).
 template <typename T, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   constexpr int D = 64, BKV = 64, NT = WAVES * 64;
-  constexpr int KS = D + 8;    // K tile row stride (halfs)
-  constexpr int VS = BKV + 8;  // V^T tile row stride (halfs)
-  constexpr int CH = BKV * D / 8 / NT;  // 16-byte chunks per thread per tensor
-  static_assert(BKV * D / 8 % NT == 0, "tile/thread mismatch");
-  using V8 = T __attribute__((ext_vector_type(8)));
+  constexpr int TILE = BKV * D * 2;     // bytes of one K or V tile
+  constexpr int NLD = TILE / 16 / NT;   // 16-byte DMA loads per thread per tensor
+  static_assert(TILE % (16 * NT) == 0, "tile/thread mismatch");
+  // Rescale the running output only when a row max grows by more than
+  // 2^8 in the exp2 domain; until then probabilities stay below 256.
+  constexpr float kRescale = 8.0f;
   using V4 = T __attribute__((ext_vector_type(4)));
-  __shared__ __attribute__((aligned(16))) T Ks[2][BKV * KS];
-  __shared__ __attribute__((aligned(16))) T Vt[2][D * VS];
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];  // [buffer][K, V]
 
   const AttnWork w = p.work[blockIdx.x];
   const int s0 = p.cu[w.seq];
   const int L = p.cu[w.seq + 1] - s0;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, g = lane >> 4;
   const int hoff = w.head * D;
   const T* Q = (const T*)p.q;
   const T* K = (const T*)p.k;
@@ -84,60 +111,70 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   u32x4_t qf[2][2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const int qr = qbase + qt * 16 + lrow;
+    const int qr = qbase + qt * 16 + lr;
 #pragma unroll
     for (int ds = 0; ds < 2; ++ds) {
       if (qr < L)
-        qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + lgrp * 8);
+        qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + g * 8);
       else
         qf[qt][ds] = u32x4_t{0, 0, 0, 0};
     }
   }
 
-  u32x4_t rk[CH], rv[CH];
-  auto gload = [&](int kv0) {
+  // DMA: load j of this thread fills LDS chunk j*NT + tid, i.e. row
+  // (j*NT + tid) / 8, holding global chunk (tid % 8) ^ (row & 7).  Rows past
+  // the sequence re-read its last key (their scores are masked to -inf, so
+  // their probabilities are exactly 0).
+  auto issue = [&](int kv0, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NT, row = c >> 3, col = (c & 7) * 8;
-      const int key = kv0 + row;
-      if (key < L) {
-        const size_t off = (size_t)(s0 + key) * p.ld + hoff + col;
-        rk[i] = *(const u32x4_t*)(K + off);
-        rv[i] = *(const u32x4_t*)(V + off);
-      } else {
-        rk[i] = u32x4_t{0, 0, 0, 0};
-        rv[i] = u32x4_t{0, 0, 0, 0};
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NT, row = c >> 3, col = (c & 7) * 8;
-      *(u32x4_t*)(&Ks[buf][row * KS + col]) = rk[i];
-      const V8 e = __builtin_bit_cast(V8, rv[i]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[buf][(col + j) * VS + row] = e[j];
+    for (int j = 0; j < NLD; ++j) {
+      const int row = (j * NT + tid) >> 3;
+      const int key = min(kv0 + row, L - 1);
+      const size_t off = (size_t)(s0 + key) * p.ld + hoff + (((tid & 7) ^ (row & 7)) << 3);
+      lds_char* kd = (lds_char*)&lds[buf][0][(j * NT + wave * 64) * 16];
+      lds_char* vd = (lds_char*)&lds[buf][1][(j * NT + wave * 64) * 16];
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(K + off),
+                                       (__attribute__((address_space(3))) void*)kd, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(V + off),
+                                       (__attribute__((address_space(3))) void*)vd, 16, 0, 0);
     }
   };
 
-  float4_t o[4][2];
+  // K fragment (S^T A operand): row kt*16 + lr, chunk ds*4 + g.
+  int koff[2];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int ds = 0; ds < 2; ++ds) koff[ds] = lr * 128 + (((ds * 4 + g) ^ (lr & 7)) << 4);
+  // V^T fragment (O^T A operand), transposing read: lane (g, s = lr) names
+  // row 4g + s/4 (+16 for keys 16..31 of a 32-key step), bytes
+  // [dt*32 + 8*(s%4), +8) of that row.
+  const int vrow = 4 * g + (lr >> 2);
+  const int vx = ((lr & 3) >> 1) ^ (vrow & 7);
+  const int vbase = vrow * 128 + (lr & 1) * 8;
+
+  float4_t o[4][2], lacc[2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+  for (int qt = 0; qt < 2; ++qt) {
+    lacc[qt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  float ms[2] = {-INFINITY, -INFINITY};  // running row max, times c
   const float c = p.scale * 1.4426950408889634f;
+  const u32x4_t ones = {AttnMfma<T>::kOnes, AttnMfma<T>::kOnes, AttnMfma<T>::kOnes,
+                        AttnMfma<T>::kOnes};
 
   const int ntiles = (L + BKV - 1) / BKV;
-  gload(0);
-  lstore(0);
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int it = 0; it < ntiles; ++it) {
     const int cur = it & 1;
     const int kv0 = it * BKV;
-    if (it + 1 < ntiles) gload(kv0 + BKV);
+    // The other buffer was last read in the previous iteration, which
+    // ended with a barrier.
+    if (it + 1 < ntiles) issue(kv0 + BKV, cur ^ 1);
+    const char* kt_lds = lds[cur][0];
+    const char* vt_lds = lds[cur][1];
 
     // S^T tiles: [key-tile][q-tile]
     float4_t s[4][2];
@@ -147,7 +184,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       s[kt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < 2; ++ds) {
-        const u32x4_t kf = *(const u32x4_t*)(&Ks[cur][(kt * 16 + lrow) * KS + ds * 32 + lgrp * 8]);
+        const u32x4_t kf = *(const u32x4_t*)(kt_lds + kt * 2048 + koff[ds]);
         AttnMfma<T>::mma(s[kt][0], kf, qf[0][ds]);
         AttnMfma<T>::mma(s[kt][1], kf, qf[1][ds]);
       }
@@ -157,38 +194,47 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (kv0 + kt * 16 + lgrp * 4 + i >= L) {
+          if (kv0 + kt * 16 + g * 4 + i >= L) {
             s[kt][0][i] = -INFINITY;
             s[kt][1][i] = -INFINITY;
           }
     }
 
-    u32x4_t pf[2][2];  // [key-step][q-tile] P^T operand
+    // Row max; lazy rescale of the running output.
+    float mx[2];
+    bool grow = false;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      float mx = s[0][qt][0];
+      float m = fmaxf(s[0][qt][0], s[0][qt][1]);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][qt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qt], mx);
-      const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
-      const float mc = m_new * c;
-      m_run[qt] = m_new;
-      float lsum = 0.f;
+        for (int i = (kt == 0 ? 2 : 0); i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
+      mx[qt] = quad_max(m) * c;
+      grow |= mx[qt] - ms[qt] > kRescale;
+    }
+    if (__any(grow)) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float mn = fmaxf(ms[qt], mx[qt]);
+        const float alpha = __builtin_amdgcn_exp2f(ms[qt] - mn);
+        ms[qt] = mn;
+        lacc[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+      }
+    }
+
+    // P^T operand [key-step][q-tile]: key k of step ks is ks*32 + 4g + k
+    // for k < 4 and ks*32 + 16 + 4g + k - 4 for k >= 4.
+    u32x4_t pf[2][2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i], c, -mc));
-          s[kt][qt][i] = e;
-          lsum += e;
-        }
-      l_run[qt] = l_run[qt] * alpha + lsum;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+        for (int i = 0; i < 4; ++i)
+          s[kt][qt][i] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i], c, -ms[qt]));
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         pf[ks][qt][0] = AttnMfma<T>::pack2(s[2 * ks][qt][0], s[2 * ks][qt][1]);
@@ -198,34 +244,34 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       }
     }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T; the row sums ride along as ones * P^T.
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int ks = 0; ks < 2; ++ks) {
+      AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
+      AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const T* vrow = &Vt[cur][(dt * 16 + lrow) * VS + ks * 32 + lgrp * 4];
-        const u32x2_t lo = *(const u32x2_t*)vrow;
-        const u32x2_t hi = *(const u32x2_t*)(vrow + 16);
+      for (int dt = 0; dt < 4; ++dt) {
+        const int col = ((dt * 2) ^ vx) << 4;
+        const u32x2_t lo = lds_read_tr16((const lds_char*)(vt_lds + ks * 4096 + vbase + col));
+        const u32x2_t hi =
+            lds_read_tr16((const lds_char*)(vt_lds + ks * 4096 + 2048 + vbase + col));
         const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
         AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
         AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
       }
     }
 
-    if (it + 1 < ntiles) lstore(cur ^ 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
   T* out = (T*)p.out;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float l = l_run[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const float inv = 1.0f / l;
-    const int qr = qbase + qt * 16 + lrow;
+    const float inv = 1.0f / lacc[qt][0];
+    const int qr = qbase + qt * 16 + lr;
     if (qr >= L) continue;
-    T* orow = out + (size_t)(s0 + qr) * p.ldo + hoff + lgrp * 4;
+    T* orow = out + (size_t)(s0 + qr) * p.ldo + hoff + g * 4;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       V4 h;
