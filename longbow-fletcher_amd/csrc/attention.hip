@@ -58,16 +58,7 @@ template <> struct AttnMfma<__bf16> {
   }
 };
 
-typedef short attn_s4 __attribute__((__vector_size__(8)));
 typedef __attribute__((address_space(3))) char lds_char;
-
-// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane block,
-// lane i receives element i%4 of the 8-byte rows addressed by lanes
-// i/4 + 4j, j = 0..3.
-__device__ inline u32x2_t lds_read_tr16(const lds_char* p) {
-  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                         (__attribute__((address_space(3))) attn_s4*)p));
-}
 
 // Max over the lanes {l, l^16, l^32, l^48} (v_permlane16/32_swap: each swap
 // returns the value pair of a lane and its xor-16 / xor-32 partner).
@@ -95,7 +86,8 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   using V4 = T __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];  // [buffer][K, V]
 
-  const AttnWork w = p.work[blockIdx.x];
+  // The query blocks of one (sequence, head) run on one XCD and share its L2.
+  const AttnWork w = p.work[xcd_group((int)blockIdx.x, (int)gridDim.x, 4)];
   const int s0 = p.cu[w.seq];
   const int L = p.cu[w.seq + 1] - s0;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -189,6 +181,25 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
         AttnMfma<T>::mma(s[kt][1], kf, qf[1][ds]);
       }
     }
+    // V^T fragments of this tile, read while the softmax runs, with the
+    // transposing LDS load ds_read_b64_tr_b16: within each 16-lane block,
+    // lane i receives element i%4 of the 8-byte rows addressed by lanes
+    // i/4 + 4j, j = 0..3.  Written as asm because the compiler cannot tell
+    // these reads from the DMA into the other buffer and would wait for it;
+    // the s_waitcnt before the P V MFMAs covers their completion.
+    u32x2_t vr[4][4];  // [dt][ks*2 + half]
+    const uint32_t vb = (uint32_t)(uintptr_t)(const lds_char*)vt_lds + vbase;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint32_t a = vb + (((dt * 2) ^ vx) << 4);
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %4\n"
+          "ds_read_b64_tr_b16 %1, %4 offset:2048\n"
+          "ds_read_b64_tr_b16 %2, %4 offset:4096\n"
+          "ds_read_b64_tr_b16 %3, %4 offset:6144\n"
+          : "=&v"(vr[dt][0]), "=&v"(vr[dt][1]), "=&v"(vr[dt][2]), "=&v"(vr[dt][3])
+          : "v"(a));
+    }
     if (kv0 + BKV > L) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -245,19 +256,23 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     }
 
     // O^T += V^T P^T; the row sums ride along as ones * P^T.
+    {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
+                     "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]),
+                     "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[2][2]), "+v"(vr[2][3]),
+                     "+v"(vr[3][0]), "+v"(vr[3][1]), "+v"(vr[3][2]), "+v"(vr[3][3]));
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
-      AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
+      for (int ks = 0; ks < 2; ++ks) {
+        AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
+        AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int col = ((dt * 2) ^ vx) << 4;
-        const u32x2_t lo = lds_read_tr16((const lds_char*)(vt_lds + ks * 4096 + vbase + col));
-        const u32x2_t hi =
-            lds_read_tr16((const lds_char*)(vt_lds + ks * 4096 + 2048 + vbase + col));
-        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-        AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
-        AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
+        for (int dt = 0; dt < 4; ++dt) {
+          const u32x2_t lo = vr[dt][ks * 2], hi = vr[dt][ks * 2 + 1];
+          const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+          AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
+          AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
+        }
       }
     }
 

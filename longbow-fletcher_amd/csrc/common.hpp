@@ -156,6 +156,19 @@ __device__ inline int xcd_remap(int bid, int nwg) {
   return (bid % kXcd) * per + bid / kXcd;
 }
 
+// Regroups a linear workgroup id so that every XCD receives runs of C
+// consecutive logical ids: within each window of 8*C dispatches (C rounds
+// over the 8 XCDs), XCD x gets logical ids [x*C, x*C + C).  The global order
+// is kept at window granularity; ids past the last full window map to
+// themselves.
+__device__ inline int xcd_group(int bid, int nwg, int C) {
+  constexpr int kXcd = 8;
+  const int win = kXcd * C;
+  if (bid >= (nwg / win) * win) return bid;
+  const int r = bid % win;
+  return bid - r + (r % kXcd) * C + r / kXcd;
+}
+
 }  // namespace fl
 
 #define FL_HIP_CHECK(expr)                                   \
