@@ -75,11 +75,13 @@ void* workspace(fl_context* ctx, size_t bytes, int* status) {
   return p;
 }
 
-const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status) {
+const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status,
+                         float scale) {
   *status = FL_OK;
-  uint32_t bits;
+  uint32_t bits, sbits;
   std::memcpy(&bits, &base, 4);
-  auto& t = ctx->rope[{bits, half}];
+  std::memcpy(&sbits, &scale, 4);
+  auto& t = ctx->rope[{bits, sbits, half}];
   if (t.cap >= max_pos && t.cs) return t.cs;
   int cap = 64;
   while (cap < max_pos) cap <<= 1;
@@ -89,14 +91,15 @@ const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int
     for (int i = 0; i < half; ++i) {
       // cpu_backend.go:790-792 (base parameterised).
       const double theta = (double)p * std::pow((double)base, -2.0 * (double)i / (double)d);
-      host[(size_t)p * half + i] = make_float2((float)std::cos(theta), (float)std::sin(theta));
+      host[(size_t)p * half + i] = make_float2((float)(std::cos(theta) * (double)scale),
+                                               (float)(std::sin(theta) * (double)scale));
     }
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     *status = hip_fail(e, "hipStreamSynchronize");
     return nullptr;
   }
-  if (t.cs) (void)hipFree(t.cs);
+  if (t.cs) ctx->rope_retired.push_back(t.cs);
   t.cs = nullptr;
   t.cap = 0;
   void* p = nullptr;
@@ -190,6 +193,7 @@ int fl_free_context(fl_context* ctx) {
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& kv : ctx->rope)
       if (kv.second.cs) (void)hipFree(kv.second.cs);
+    for (float2* p : ctx->rope_retired) (void)hipFree(p);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
@@ -215,6 +219,8 @@ int fl_set_device(fl_context* ctx, int device) {
   if (ctx->flag) (void)hipFree(ctx->flag);
   for (auto& kv : ctx->rope)
     if (kv.second.cs) (void)hipFree(kv.second.cs);
+  for (float2* p : ctx->rope_retired) (void)hipFree(p);
+  ctx->rope_retired.clear();
   ctx->ws = nullptr;
   ctx->ws_size = 0;
   ctx->flag = nullptr;
@@ -654,7 +660,8 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
   const AttnWork* dwork = (const AttnWork*)(ws + cu_bytes);
   if (fast16) {
     FL_CHECK_LAUNCH(launch_attention_flash(dtype, q, k, v, hidden, out, hidden, dcu, dwork,
-                                           (int)work.size(), scale, waves, ctx->stream));
+                                           (int)work.size(), scale, waves, false,
+                                           (max_len + bq - 1) / bq, ctx->stream));
   } else if (fast32) {
     FL_CHECK_LAUNCH(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, hidden,
                                          (float*)out, hidden, dcu, dwork, (int)work.size(), scale,

@@ -13,8 +13,9 @@
 // V^T operand is read with the gfx950 transposing LDS load.  A query
 // column's scores of a key tile live in the 4 lanes {q, q+16, q+32, q+48};
 // its row max is two permlane swaps and its row sum comes out of an extra
-// MFMA against a ones operand, so the softmax costs one FMA, one exp2, half
-// a max and half a pack per score.
+// MFMA against a ones operand; with Q pre-scaled, the offset by the running
+// max rides in the score MFMA's accumulator, so the softmax costs one exp2,
+// half a max and half a pack per score.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -30,6 +31,7 @@ struct AttnParams {
   const int* cu;
   const AttnWork* work;
   float scale;
+  int group;  // consecutive work items per XCD (query blocks of one sequence-head)
 };
 
 template <typename T> struct AttnMfma;
@@ -74,7 +76,13 @@ __device__ inline float quad_max(float v) {
 // One workgroup = WAVES waves x 32 query rows of one (sequence, head); key /
 // value tiles of 64 rows are double-buffered in LDS.  A tile is 64 rows of
 // 128 bytes; 16-byte chunk c of row r sits at chunk c ^ (r & 7).
-template <typename T, int WAVES>
+//
+// Scores are kept relative to a running row maximum m in the exp2 domain:
+// x = s * scale * log2(e) - m, p = exp2(x).  PRE: Q arrives multiplied by
+// scale * log2(e) (the encoder's QKV epilogue does it), so the first score
+// MFMA starts from the accumulator -m and produces x directly; otherwise x
+// takes one FMA per score.
+template <typename T, int WAVES, bool PRE>
 __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   constexpr int D = 64, BKV = 64, NT = WAVES * 64;
   constexpr int TILE = BKV * D * 2;     // bytes of one K or V tile
@@ -87,7 +95,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];  // [buffer][K, V]
 
   // The query blocks of one (sequence, head) run on one XCD and share its L2.
-  const AttnWork w = p.work[xcd_group((int)blockIdx.x, (int)gridDim.x, 4)];
+  const AttnWork w = p.work[xcd_group((int)blockIdx.x, (int)gridDim.x, p.group)];
   const int s0 = p.cu[w.seq];
   const int L = p.cu[w.seq + 1] - s0;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -114,15 +122,25 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   }
 
   // DMA: load j of this thread fills LDS chunk j*NT + tid, i.e. row
-  // (j*NT + tid) / 8, holding global chunk (tid % 8) ^ (row & 7).  Rows past
-  // the sequence re-read its last key (their scores are masked to -inf, so
-  // their probabilities are exactly 0).
+  // (j*NT + tid) / 8, holding global chunk (tid % 8) ^ (row & 7).  In the
+  // last tile, rows past the sequence re-read its last key (their scores are
+  // masked to -inf, so their probabilities are exactly 0).
+  const size_t ldk = (size_t)p.ld;
+  size_t goff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) {
+    const int row = (j * NT + tid) >> 3;
+    goff[j] = (size_t)(s0 + row) * ldk + hoff + (((tid & 7) ^ (row & 7)) << 3);
+  }
   auto issue = [&](int kv0, int buf) __attribute__((always_inline)) {
+    const bool tail = kv0 + BKV > L;
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
-      const int row = (j * NT + tid) >> 3;
-      const int key = min(kv0 + row, L - 1);
-      const size_t off = (size_t)(s0 + key) * p.ld + hoff + (((tid & 7) ^ (row & 7)) << 3);
+      size_t off = goff[j] + (size_t)kv0 * ldk;
+      if (tail) {
+        const int row = (j * NT + tid) >> 3;
+        off -= (size_t)max(kv0 + row - (L - 1), 0) * ldk;
+      }
       lds_char* kd = (lds_char*)&lds[buf][0][(j * NT + wave * 64) * 16];
       lds_char* vd = (lds_char*)&lds[buf][1][(j * NT + wave * 64) * 16];
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(K + off),
@@ -150,7 +168,9 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
-  float ms[2] = {-INFINITY, -INFINITY};  // running row max, times c
+  // Running row max m (exp2 domain); 0 until the first tile sets it.
+  float ms[2] = {0.f, 0.f};
+  float4_t cinit[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
   const float c = p.scale * 1.4426950408889634f;
   const u32x4_t ones = {AttnMfma<T>::kOnes, AttnMfma<T>::kOnes, AttnMfma<T>::kOnes,
                         AttnMfma<T>::kOnes};
@@ -168,18 +188,26 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     const char* kt_lds = lds[cur][0];
     const char* vt_lds = lds[cur][1];
 
-    // S^T tiles: [key-tile][q-tile]
+    // Relative scores x, transposed: [key-tile][q-tile]
     float4_t s[4][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      s[kt][0] = float4_t{0.f, 0.f, 0.f, 0.f};
-      s[kt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+      s[kt][0] = PRE ? cinit[0] : float4_t{0.f, 0.f, 0.f, 0.f};
+      s[kt][1] = PRE ? cinit[1] : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < 2; ++ds) {
         const u32x4_t kf = *(const u32x4_t*)(kt_lds + kt * 2048 + koff[ds]);
         AttnMfma<T>::mma(s[kt][0], kf, qf[0][ds]);
         AttnMfma<T>::mma(s[kt][1], kf, qf[1][ds]);
       }
+    }
+    if constexpr (!PRE) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[kt][qt][i] = fmaf(s[kt][qt][i], c, -ms[qt]);
     }
     // V^T fragments of this tile, read while the softmax runs, with the
     // transposing LDS load ds_read_b64_tr_b16: within each 16-lane block,
@@ -211,9 +239,10 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
           }
     }
 
-    // Row max; lazy rescale of the running output.
+    // Row max; lazy rescale of the running output.  The first tile always
+    // sets m; later tiles move it only when a row max grows past 2^8.
     float mx[2];
-    bool grow = false;
+    bool grow = it == 0;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       float m = fmaxf(s[0][qt][0], s[0][qt][1]);
@@ -221,18 +250,23 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = (kt == 0 ? 2 : 0); i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
-      mx[qt] = quad_max(m) * c;
-      grow |= mx[qt] - ms[qt] > kRescale;
+      mx[qt] = quad_max(m);
+      grow |= mx[qt] > kRescale;
     }
     if (__any(grow)) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float mn = fmaxf(ms[qt], mx[qt]);
-        const float alpha = __builtin_amdgcn_exp2f(ms[qt] - mn);
-        ms[qt] = mn;
-        lacc[qt] *= alpha;
+        const float shift = it == 0 ? mx[qt] : fmaxf(mx[qt], 0.f);
+        ms[qt] += shift;
+        cinit[qt] = float4_t{-ms[qt], -ms[qt], -ms[qt], -ms[qt]};
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+        for (int kt = 0; kt < 4; ++kt) s[kt][qt] -= shift;
+        if (it > 0) {
+          const float alpha = __builtin_amdgcn_exp2f(-shift);
+          lacc[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+        }
       }
     }
 
@@ -245,7 +279,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          s[kt][qt][i] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i], c, -ms[qt]));
+          s[kt][qt][i] = __builtin_amdgcn_exp2f(s[kt][qt][i]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         pf[ks][qt][0] = AttnMfma<T>::pack2(s[2 * ks][qt][0], s[2 * ks][qt][1]);
@@ -297,26 +331,29 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   }
 }
 
+template <typename T>
+static void launch_flash_typed(const AttnParams& p, int n_work, int waves, bool prescaled,
+                               hipStream_t stream) {
+  const dim3 grid(n_work);
+  if (waves == 2) {
+    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 2, true>), grid, dim3(128), 0, stream, p);
+    else hipLaunchKernelGGL((attn_flash_kernel<T, 2, false>), grid, dim3(128), 0, stream, p);
+  } else {
+    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 4, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((attn_flash_kernel<T, 4, false>), grid, dim3(256), 0, stream, p);
+  }
+}
+
 hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
                                   const AttnWork* work, int n_work, float scale, int waves,
-                                  hipStream_t stream) {
+                                  bool q_prescaled, int xcd_group_size, hipStream_t stream) {
   if (n_work <= 0) return hipSuccess;
-  AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale};
-  dim3 grid(n_work);
-  if (dtype == F16) {
-    if (waves == 2)
-      hipLaunchKernelGGL((attn_flash_kernel<_Float16, 2>), grid, dim3(128), 0, stream, p);
-    else
-      hipLaunchKernelGGL((attn_flash_kernel<_Float16, 4>), grid, dim3(256), 0, stream, p);
-  } else if (dtype == BF16) {
-    if (waves == 2)
-      hipLaunchKernelGGL((attn_flash_kernel<__bf16, 2>), grid, dim3(128), 0, stream, p);
-    else
-      hipLaunchKernelGGL((attn_flash_kernel<__bf16, 4>), grid, dim3(256), 0, stream, p);
-  } else {
-    return hipErrorInvalidValue;
-  }
+  const AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale,
+                     std::max(1, std::min(xcd_group_size, 32))};
+  if (dtype == F16) launch_flash_typed<_Float16>(p, n_work, waves, q_prescaled, stream);
+  else if (dtype == BF16) launch_flash_typed<__bf16>(p, n_work, waves, q_prescaled, stream);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -457,7 +494,7 @@ hipError_t launch_attention_f32(const float* q, const float* k, const float* v, 
                                 const AttnWork* work, int n_work, float scale, int math,
                                 hipStream_t stream) {
   if (n_work <= 0) return hipSuccess;
-  AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale};
+  AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale, 1};
   if (math == MATH_REFERENCE)
     hipLaunchKernelGGL(attn_f32_kernel<MATH_REFERENCE>, dim3(n_work), dim3(256), 0, stream, p);
   else

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -38,7 +39,11 @@ struct fl_context {
     float2* cs = nullptr;
     int cap = 0;
   };
-  std::map<std::pair<uint32_t, int>, RopeTable> rope;
+  // keyed by (bits of base, bits of scale, half)
+  std::map<std::tuple<uint32_t, uint32_t, int>, RopeTable> rope;
+  // Tables replaced by larger ones stay allocated until teardown: a model
+  // keeps the pointer it was handed for its own lengths.
+  std::vector<float2*> rope_retired;
 };
 
 namespace fl {
@@ -51,7 +56,10 @@ int activate(fl_context* ctx);
 void* workspace(fl_context* ctx, size_t bytes, int* status);
 // Device-side (cos, sin) table for positions [0, max_pos) (float64 angles,
 // cpu_backend.go:790-792 with the base as a parameter).
-const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status);
+// (cos, sin) of position p and pair i, times `scale`, at [p * half + i] for
+// p < max_pos: angles and products in float64, cast to float32 once.
+const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status,
+                         float scale = 1.0f);
 int device_alloc(fl_context* ctx, size_t bytes, void** out);
 void device_free(fl_context* ctx, void* p);
 

@@ -958,7 +958,8 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmPara
       for (int f = 0; f < 4; ++f) v[f] = biased(f, t);
       if (nbase < p.epi.rope_cols) {
 #pragma clang fp contract(off)
-        const float4_t* cs = (const float4_t*)(p.epi.rope_cs + (size_t)p.epi.pos[mc] * 32 + g * 8);
+        const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
+        const float4_t* cs = (const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8);
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
 #pragma unroll
@@ -984,6 +985,10 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmPara
       float4_t v[4];
 #pragma unroll
       for (int f = 0; f < 4; ++f) v[f] = act4<EPI, MATH>(biased(f, t));
+      if (nbase < p.epi.q_cols) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) v[f] *= p.epi.q_scale;
+      }
       if (ok) {
         store8<T>(crow + nbase + g * 16, v[0], v[1]);
         store8<T>(crow + nbase + g * 16 + 8, v[2], v[3]);
@@ -1434,8 +1439,13 @@ bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, c
     if (lda % 8 || ldb % 8 || ldc % 8) return false;
     if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C | (uintptr_t)epi.bias) & 15) return false;
     if (epi.kind == EPI_ROPE && (epi.rope_cols % 64 || !epi.pos || !epi.rope_cs)) return false;
+    if (epi.q_cols && (epi.q_cols % 64 || (epi.kind != EPI_STORE && epi.kind != EPI_ROPE)))
+      return false;
+    if (epi.q_cols && epi.kind == EPI_ROPE && (!epi.rope_cs_q || epi.q_cols > epi.rope_cols))
+      return false;
     return true;
   }
+  if (epi.q_cols) return false;  // only the ping-pong epilogues scale a query block
   if (epi.layout != (epi.kind == EPI_SWIGLU ? PACK_SWIGLU16 : PACK_PLAIN)) return false;
   const int esz = dtype == F32 ? 4 : 2;
   const int epc = 16 / esz;

@@ -64,6 +64,14 @@ struct GemmEpilogue {
   const int* pos = nullptr;        // [M] position of each row in its sequence
   int rope_cols = 0;
   int layout = PACK_PLAIN;         // PackLayout of B and bias
+  // Output columns [0, q_cols) are multiplied by q_scale last (the query
+  // block of a fused QKV projection, pre-scaled for the flash kernel).  The
+  // ping-pong kernel's STORE epilogue multiplies; its RoPE epilogue rotates
+  // those columns with rope_cs_q, the table times q_scale.  gemm_nt_supported
+  // rejects q_cols elsewhere.
+  int q_cols = 0;
+  float q_scale = 1.0f;
+  const float2* rope_cs_q = nullptr;
 };
 
 // The packing the ping-pong GEMM needs for this problem, or -1 when that
@@ -104,10 +112,13 @@ struct AttnWork {
   int pad;
 };
 // Flash attention (exact math, online softmax) for head_dim 64, 16-bit types.
+// q_prescaled: Q already holds q * scale * log2(e) (GemmEpilogue::q_scale).
+// xcd_group_size: consecutive work items (the query blocks of one sequence
+// and head) kept on one XCD, clamped to [1, 32].
 hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
                                   const AttnWork* work, int n_work, float scale, int waves,
-                                  hipStream_t stream);
+                                  bool q_prescaled, int xcd_group_size, hipStream_t stream);
 // Two-pass attention (exact row max, then reference ExpFast or exp) for
 // head_dim 64 fp32.
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v, int ldqkv,

@@ -89,7 +89,10 @@ struct fl_model {
   std::vector<int64_t> last_lengths;
   int64_t T = 0;
   int n_work = 0, max_len = 0, waves = 4;
+  int qblocks = 1;            // query blocks of the longest sequence (flash work items per head)
+  bool q_prescaled = false;   // QKV epilogue multiplies Q by scale * log2(e) for the flash kernel
   const float2* rope_cs = nullptr;
+  const float2* rope_cs_q = nullptr;  // rope_cs * scale * log2(e), for a pre-scaled Q
 
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;
@@ -100,6 +103,10 @@ struct fl_model {
 };
 
 namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Attention scale 1/float32(sqrt(d)) (bert.go:643).
+float attn_scale(int hd) { return 1.0f / (float)std::sqrt((double)hd); }
 
 int track_alloc(fl_model* m, size_t bytes, void** out) {
   int st = device_alloc(m->ctx, bytes, out);
@@ -282,6 +289,11 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
       int st;
       m->rope_cs = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st);
       if (st) return st;
+      if (m->q_prescaled) {
+        m->rope_cs_q = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st,
+                                  attn_scale(m->hd) * kLog2e);
+        if (st) return st;
+      }
     }
     hipStream_t s = m->ctx->stream;
     M_CHECK(hipMemcpyAsync(m->cu, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, s));
@@ -293,6 +305,7 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
     m->last_lengths.assign(lengths, lengths + nseq);
     m->n_work = (int)work.size();
     m->waves = waves;
+    m->qblocks = (max_len + bq - 1) / bq;
   }
   m->T = T;
   m->max_len = max_len;
@@ -339,19 +352,24 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
         e.pos = m->pos32;
         e.rope_cols = 2 * H;
       }
+      if (m->q_prescaled) {
+        e.q_cols = H;
+        e.q_scale = attn_scale(m->hd) * kLog2e;
+        e.rope_cs_q = m->rope_cs_q;
+      }
       M_ST(gemm(m, m->mfma_qkv, m->X, w.wqkv, m->QKV, Ti, 3 * H, H, e));
       if (m->rope && !m->rope_fused)
         M_CHECK(launch_rope(dt, m->QKV, Ti, 2 * m->heads, m->hd, 3 * H, m->pos32, m->rope_cs, s));
     }
     {
       ProfScope ps(m, P_ATTN);
-      const float scale = 1.0f / (float)std::sqrt((double)m->hd);  // bert.go:643
+      const float scale = attn_scale(m->hd);
       const char* q = (const char*)m->QKV;
       const void* k = q + (size_t)H * m->esz;
       const void* v = q + (size_t)2 * H * m->esz;
       if (m->hd == 64 && dt != FL_F32)
         M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, m->CTX, H, m->cu, m->work, m->n_work,
-                                       scale, m->waves, s));
+                                       scale, m->waves, m->q_prescaled, m->qblocks, s));
       else if (m->hd == 64)
         M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
                                      (float*)m->CTX, H, m->cu, m->work, m->n_work, scale,
@@ -473,6 +491,10 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
                           : pick(m->mfma_up, m->Ni, m->H, EPI_GELU, PACK_PLAIN);
     if (m->swiglu && !m->mfma_up) m->lay_up = PACK_PLAIN;
     m->lay_down = pick(m->mfma_down, m->H, m->I, EPI_STORE, PACK_PLAIN);
+    // The flash kernel takes Q pre-scaled when the QKV projection runs on the
+    // ping-pong kernel, whose epilogue applies the scale.
+    m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
+                     m->H % 64 == 0;
   }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
