@@ -15,7 +15,12 @@ namespace fl {
 // Loads VEC consecutive elements starting at p as floats.
 template <typename T, int VEC>
 __device__ inline void load_vec(const T* p, float* out) {
-  if constexpr (VEC == 4 && sizeof(T) == 2) {
+  if constexpr (VEC == 8 && sizeof(T) == 2) {
+    using V8 = T __attribute__((ext_vector_type(8)));
+    V8 v = *(const V8*)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = to_f(v[i]);
+  } else if constexpr (VEC == 4 && sizeof(T) == 2) {
     using V4 = T __attribute__((ext_vector_type(4)));
     V4 v = *(const V4*)p;
 #pragma unroll
@@ -32,7 +37,13 @@ __device__ inline void load_vec(const T* p, float* out) {
 
 template <typename T, int VEC>
 __device__ inline void store_vec(T* p, const float* in) {
-  if constexpr (VEC == 4 && sizeof(T) == 2) {
+  if constexpr (VEC == 8 && sizeof(T) == 2) {
+    using V8 = T __attribute__((ext_vector_type(8)));
+    V8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = from_f<T>(in[i]);
+    *(V8*)p = v;
+  } else if constexpr (VEC == 4 && sizeof(T) == 2) {
     using V4 = T __attribute__((ext_vector_type(4)));
     V4 v;
 #pragma unroll
@@ -46,9 +57,17 @@ __device__ inline void store_vec(T* p, const float* in) {
   }
 }
 
-// Normalises x[NCH][VEC] (this lane's share of one row; `valid` masks the
-// tail) in place.
-template <int NCH, int VEC>
+// Sum over the LPR consecutive lanes that share a row.
+template <int LPR>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Normalises x[NCH][VEC] (this lane's share of one row, spread over LPR
+// lanes; `valid` masks the tail) in place.
+template <int NCH, int VEC, int LPR = 64>
 __device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], int cols,
                                const float* gamma, const float* beta, const int (&col0)[NCH],
                                float eps) {
@@ -59,7 +78,7 @@ __device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], i
     if (valid[c])
 #pragma unroll
       for (int i = 0; i < VEC; ++i) s += x[c][i];
-  s = wave_sum(s);
+  s = group_sum<LPR>(s);
   const float mean = s / (float)cols;
   float v = 0.f;
 #pragma unroll
@@ -70,7 +89,7 @@ __device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], i
         const float d = x[c][i] - mean;
         v += d * d;
       }
-  v = wave_sum(v);
+  v = group_sum<LPR>(v);
   const float var = v / (float)cols;
   const float inv = 1.0f / (float)sqrt((double)(var + eps));
 #pragma unroll
@@ -113,6 +132,54 @@ layernorm_kernel(T* t, const T* residual, int rows, int cols, const float* gamma
     if (valid[c]) store_vec<T, VEC>(tr + col0[c], x[c]);
 }
 
+// 16-byte vectors, LPR lanes per row (64 / LPR rows per wave): for H = 768
+// in 16 bits, half a wave per row and three 16-byte loads per lane and
+// tensor, so twice the rows per wave are in flight.
+template <typename T, int LPR, int NCH, int VEC>
+__global__ void __launch_bounds__(256)
+layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* gamma,
+                      const float* beta, float eps) {
+  constexpr int RPW = 64 / LPR;
+  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + ((threadIdx.x & 63) / LPR);
+  const int lane = threadIdx.x % LPR;
+  if (row >= rows) return;
+  T* tr = t + (size_t)row * cols;
+  const T* rr = residual ? residual + (size_t)row * cols : nullptr;
+  float x[NCH][VEC];
+  bool valid[NCH];
+  int col0[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    col0[c] = (lane + c * LPR) * VEC;
+    valid[c] = col0[c] < cols;
+    if (valid[c]) load_vec<T, VEC>(tr + col0[c], x[c]);
+  }
+  if (rr) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (valid[c]) {
+        float r[VEC];
+        load_vec<T, VEC>(rr + col0[c], r);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + r[i];
+      }
+  }
+  ln_core<NCH, VEC, LPR>(x, valid, cols, gamma, beta, col0, eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c]) store_vec<T, VEC>(tr + col0[c], x[c]);
+}
+
+template <typename T, int LPR, int NCH, int VEC>
+static hipError_t ln_rows_launch(void* t, const void* res, int rows, int cols, const float* g,
+                                 const float* b, float eps, hipStream_t s) {
+  constexpr int rows_per_block = 4 * (64 / LPR);
+  hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC>),
+                     dim3((rows + rows_per_block - 1) / rows_per_block), dim3(256), 0, s, (T*)t,
+                     (const T*)res, rows, cols, g, b, eps);
+  return hipGetLastError();
+}
+
 template <typename T, int NCH, int VEC>
 static hipError_t ln_launch(void* t, const void* res, int rows, int cols, const float* g,
                             const float* b, float eps, hipStream_t s) {
@@ -124,6 +191,16 @@ static hipError_t ln_launch(void* t, const void* res, int rows, int cols, const 
 template <typename T>
 static hipError_t ln_typed(void* t, const void* res, int rows, int cols, const float* g,
                            const float* b, float eps, hipStream_t s) {
+  constexpr int V16 = 16 / sizeof(T);  // elements per 16-byte vector
+  if (cols % (32 * V16) == 0 && cols <= 4 * 32 * V16 &&
+      (((uintptr_t)t | (uintptr_t)res) % 16) == 0) {
+    switch (cols / (32 * V16)) {
+      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, rows, cols, g, b, eps, s);
+      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, rows, cols, g, b, eps, s);
+      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, rows, cols, g, b, eps, s);
+      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, rows, cols, g, b, eps, s);
+    }
+  }
   if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res) % (4 * sizeof(T)) == 0)) {
     const int nch = (cols / 4 + 63) / 64;
     if (nch <= 1) return ln_launch<T, 1, 4>(t, res, rows, cols, g, b, eps, s);
