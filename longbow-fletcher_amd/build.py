@@ -34,8 +34,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object
 # Per-file flags.  gemm.hip: keep MFMA accumulators in architectural VGPRs
 # (the accumulator-register form made the allocator copy accumulators every
 # K step).
+# attention.hip: also no NaN-quieting before every max of the softmax row
+# reductions (NaN inputs still propagate through exp2 and the P V products).
 PER_FILE = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-            "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+            "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"]}
 
 
 def _compile(src: pathlib.Path) -> pathlib.Path:
