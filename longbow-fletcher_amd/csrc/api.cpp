@@ -434,7 +434,14 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   // Scratch layout: [fp32 bias][packed W][unfused product]
   const size_t bias_bytes = bias ? ((size_t)out_cols * 4 + 255) / 256 * 256 : 0;
   const size_t w_bytes = ((size_t)out_cols * in_cols * esz + 255) / 256 * 256;
-  const bool unfused = act == FL_ACT_SWIGLU || act == FL_ACT_SOFTMAX;
+  // SwiGLU runs in the ping-pong kernel's epilogue when that kernel takes the
+  // shape (16-bit, exact math); otherwise the full product is written first.
+  const bool w_rows_ok =
+      w_layout == FL_W_IN_OUT || !(((uintptr_t)w | ((size_t)in_cols * esz)) & 15);
+  const bool fused_swiglu =
+      act == FL_ACT_SWIGLU && w_rows_ok && !(((uintptr_t)x | (uintptr_t)out) & 15) &&
+      gemm_pp_layout(dtype, out_cols, in_cols, EPI_SWIGLU, math, bias != nullptr) >= 0;
+  const bool unfused = (act == FL_ACT_SWIGLU && !fused_swiglu) || act == FL_ACT_SOFTMAX;
   const size_t y_bytes = unfused ? (size_t)rows * out_cols * esz : 0;
   int st;
   // [packed fp32 bias][fp32 bias staging][packed W][unfused product]
@@ -444,14 +451,14 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   const int epi_act = (act == FL_ACT_GELU || act == FL_ACT_TANH) ? act : FL_ACT_IDENTITY;
 
   GemmEpilogue epi;
-  epi.kind = epi_act == FL_ACT_GELU ? EPI_GELU : (epi_act == FL_ACT_TANH ? EPI_TANH : EPI_STORE);
+  epi.kind = fused_swiglu ? EPI_SWIGLU
+                          : (epi_act == FL_ACT_GELU ? EPI_GELU
+                                                    : (epi_act == FL_ACT_TANH ? EPI_TANH : EPI_STORE));
   epi.math = math;
   // The ping-pong kernel takes W and the bias in its own row order.
   const int lay = gemm_pp_layout(dtype, out_cols, in_cols, epi.kind, math, bias != nullptr);
-  if (lay >= 0 && w_layout == FL_W_OUT_IN && (((uintptr_t)w | ((size_t)in_cols * esz)) & 15))
-    epi.layout = PACK_PLAIN;
-  else
-    epi.layout = lay >= 0 ? lay : PACK_PLAIN;
+  epi.layout = lay >= 0 && w_rows_ok ? lay : PACK_PLAIN;
+  const int ldy = fused_swiglu ? out_cols / 2 : out_cols;
   float* bias32 = nullptr;      // packed order for the MFMA kernels
   float* bias_plain = nullptr;  // column order for the generic kernel
   if (bias) {
@@ -464,7 +471,7 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   const void* wnk = w;
   void* pk = ws + 2 * bias_bytes;
   bool mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, pk, in_cols, y,
-                                out_cols, epi);
+                                ldy, epi);
   if (mfma && w_layout == FL_W_IN_OUT) {
     FL_CHECK_LAUNCH(launch_transpose(dtype, w, in_cols, out_cols, pk, epi.layout, ctx->stream));
     wnk = pk;
@@ -474,17 +481,19 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
     wnk = pk;
   }
   if (mfma) mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, wnk, in_cols, y,
-                                     out_cols, epi);
+                                     ldy, epi);
   if (mfma) {
-    FL_CHECK_LAUNCH(launch_gemm_nt(dtype, x, in_cols, wnk, in_cols, y, out_cols, rows, out_cols,
+    FL_CHECK_LAUNCH(launch_gemm_nt(dtype, x, in_cols, wnk, in_cols, y, ldy, rows, out_cols,
                                    in_cols, epi, ctx->stream));
+  } else if (fused_swiglu) {
+    return fail(FL_ERR_UNSUPPORTED, "fl_linear: SwiGLU operands not 16-byte aligned");
   } else {
     const int tb = w_layout == FL_W_OUT_IN;
     FL_CHECK_LAUNCH(launch_gemm_generic(dtype, 0, tb, rows, out_cols, in_cols, 1.0f, x, in_cols,
                                         w, tb ? in_cols : out_cols, y, out_cols, bias_plain, epi_act,
                                         math, ctx->stream));
   }
-  if (act == FL_ACT_SWIGLU) {
+  if (act == FL_ACT_SWIGLU && !fused_swiglu) {
     FL_CHECK_LAUNCH(launch_swiglu(dtype, y, rows, out_cols / 2, out, math, ctx->stream));
   } else if (act == FL_ACT_SOFTMAX) {
     FL_CHECK_LAUNCH(hipMemcpyAsync(out, y, (size_t)rows * out_cols * esz, hipMemcpyDeviceToDevice,

@@ -26,6 +26,9 @@
 #ifndef FL_GEMM_PP_NS
 #define FL_GEMM_PP_NS 4
 #endif
+#ifndef FL_GEMM_PP_SPREAD
+#define FL_GEMM_PP_SPREAD 8
+#endif
 #ifndef FL_GEMM_PP_GROUP_M
 #define FL_GEMM_PP_GROUP_M 8
 #endif
@@ -1000,6 +1003,54 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmPara
   }
 }
 
+// SwiGLU epilogue: row blocks t < 8 - NSTG are stored at once; the packed
+// outputs of the last NSTG row blocks go to out + (t - 8 + NSTG)*1024 +
+// lane*16 in LDS, and the kernel stores them to C one row block per compute
+// tick, so a finished tile's stores do not reach the memory pipeline in one
+// burst ahead of the DMA of the next steps.
+template <typename T, int MATH, int NSTG>
+__device__ __attribute__((always_inline)) inline void pp_swiglu_stage(const GemmParams& p,
+                                                                     const float4_t (&acc)[4][8],
+                                                                     int m0, int nbase, int lane,
+                                                                     char* out) {
+  asm volatile("" : "+v"(lane));
+  const int g = lane >> 4;
+  const float* bias = p.epi.bias;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    float4_t o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
+      float4_t gt = acc[2 * h][t], up = acc[2 * h + 1][t];
+      if (bias) {
+        gt += *(const float4_t*)(bias + nbase + (2 * h) * 16 + g * 4);
+        up += *(const float4_t*)(bias + nbase + (2 * h + 1) * 16 + g * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(gt[i]) * up[i];
+    }
+    u32x4_t v;
+    if constexpr (Elem<T>::dtype == F16) {
+      const half8_t hh = {(_Float16)o[0][0], (_Float16)o[0][1], (_Float16)o[0][2],
+                          (_Float16)o[0][3], (_Float16)o[1][0], (_Float16)o[1][1],
+                          (_Float16)o[1][2], (_Float16)o[1][3]};
+      v = __builtin_bit_cast(u32x4_t, hh);
+    } else {
+      const bf16x8_t hh = {(__bf16)o[0][0], (__bf16)o[0][1], (__bf16)o[0][2], (__bf16)o[0][3],
+                           (__bf16)o[1][0], (__bf16)o[1][1], (__bf16)o[1][2], (__bf16)o[1][3]};
+      v = __builtin_bit_cast(u32x4_t, hh);
+    }
+    if (t >= 8 - NSTG) {
+      *(u32x4_t*)(out + (t - (8 - NSTG)) * 1024 + lane * 16) = v;
+    } else {
+      const int m = m0 + t * 16 + (lane & 15);
+      if (m < p.M) *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + nbase / 2 + g * 8) = v;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Ping-pong 16-bit GEMM: 256x256 tiles, 8 waves in two groups of four (one
 // wave of each group per SIMD), NS LDS stages of BK-deep K slices, one
@@ -1045,8 +1096,14 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   constexpr int NLD = STAGE / 1024 / 8;        // 1 KB DMA loads per wave per step
   constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
   static_assert(BK == 32 || BK == 64, "BK 32 or 64");
-  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS stages");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  // SwiGLU stages NSTG of each wave's 8 finished row blocks in LDS (1 KB
+  // each) and stores them over the following compute ticks.  (Staging half
+  // of the plain STORE epilogue's rows, at the cost of a stage, was slower.)
+  constexpr bool STAGE_OUT = EPI == EPI_SWIGLU;
+  constexpr int NSTG = FL_GEMM_PP_SPREAD;
+  constexpr int OUTW = STAGE_OUT ? NSTG * 1024 : 0;
+  static_assert(NS >= 2 && NS * STAGE + 8 * OUTW <= 160 * 1024, "LDS stages");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 8 * OUTW];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1148,7 +1205,31 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   constexpr int NMF = KS * FN * TM;
   constexpr int PER = NMF / NLD;
   static_assert(NMF % NLD == 0, "loads spread evenly over the MFMAs");
+  // Staged outputs not yet stored: staged block NSTG - pst_left is next; its
+  // 16 bytes per lane are read from LDS in the memory tick (pv) and stored
+  // first thing in the following compute tick, ahead of that tick's DMA.
+  char* outw = lds + NS * STAGE + wave * OUTW;
+  int pst_left = 0, pst_row0 = 0, pst_col = 0, stored = 0;
+  u32x4_t pv = {0, 0, 0, 0};
+  auto fetch_pending = [&]() __attribute__((always_inline)) {
+    if constexpr (STAGE_OUT) {
+      if (pst_left > 0) pv = *(const u32x4_t*)(outw + (NSTG - pst_left) * 1024 + lane * 16);
+    }
+  };
+  auto store_pending = [&]() __attribute__((always_inline)) {
+    stored = 0;
+    if constexpr (STAGE_OUT) {
+      if (pst_left > 0) {
+        // staged block NSTG - pst_left is row block TM - pst_left
+        const int m = pst_row0 + (TM - pst_left) * 16 + (lane & 15);
+        if (m < p.M) *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + pst_col) = pv;
+        --pst_left;
+        stored = 1;
+      }
+    }
+  };
   auto compute = [&](char* stage) __attribute__((always_inline)) {
+    store_pending();
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -1179,7 +1260,16 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   auto epilogue = [&](int ti) __attribute__((always_inline)) {
     int m0, n0;
     coords(ti, m0, n0);
-    pp_epilogue<T, EPI, MATH, EPI != EPI_ROPE>(p, acc, m0, n0 + wn * WTN, grp * WTM, lane);
+    // The previous tile's NSTG staged row blocks went out in the compute ticks
+    // since its epilogue (gemm_pp_layout requires K / BK >= 8).
+    if constexpr (EPI == EPI_SWIGLU) {
+      pp_swiglu_stage<T, MATH, NSTG>(p, acc, m0 + grp * WTM, n0 + wn * WTN, lane, outw);
+      pst_left = NSTG;
+      pst_row0 = m0 + grp * WTM;
+      pst_col = (n0 + wn * WTN) / 2 + (lane >> 4) * 8;
+    } else {
+      pp_epilogue<T, EPI, MATH, EPI != EPI_ROPE>(p, acc, m0, n0 + wn * WTN, grp * WTM, lane);
+    }
     zero_acc();
     // Keep the next fragment reads (and their registers) after the epilogue.
     asm volatile("" ::: "memory");
@@ -1198,8 +1288,23 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   // every tick issues NLD of them, so "step s+1 landed" is "at most the
   // loads of the NS-2 later steps outstanding".  Epilogue stores also count
   // in vmcnt; they can only make the wait longer, never shorter.
+  // A compute tick that stored a staged row block issued that store before
+  // its DMA loads, so it too may stay outstanding.
   auto wait_next = [&]() __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD * (NS - 2)) : "memory");
+    if constexpr (STAGE_OUT) {
+      asm volatile(
+          "s_cmp_eq_u32 %0, 0\n"
+          "s_cbranch_scc1 1f\n"
+          "s_waitcnt vmcnt(%1)\n"
+          "s_branch 2f\n"
+          "1:\n"
+          "s_waitcnt vmcnt(%2)\n"
+          "2:" ::"s"(stored),
+          "n"(NLD * (NS - 2) + 1), "n"(NLD * (NS - 2))
+          : "memory", "scc");
+    } else {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD * (NS - 2)) : "memory");
+    }
   };
 
   int ck = 0, ctile = 0;       // K step / tile of the next compute
@@ -1213,6 +1318,7 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
         pending = false;
       }
       read_frags(lds + (s % NS) * STAGE);
+      fetch_pending();
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       pp_barrier();
       // tick 2s+1: compute step s, DMA of step s+NS-1
@@ -1247,9 +1353,11 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
         epilogue(ptile);
         pending = false;
         read_frags(lds + (s % NS) * STAGE);
+        fetch_pending();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       } else {
         read_frags(lds + (s % NS) * STAGE);
+        fetch_pending();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         wait_next();
       }
@@ -1260,6 +1368,11 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
     ptile = ctile;
   }
   if (pending) epilogue(ptile);
+#pragma unroll
+  for (int t = 0; t < NSTG; ++t) {
+    fetch_pending();
+    store_pending();
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
@@ -1340,8 +1453,11 @@ template <typename T, int EPI, int MATH>
 static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
   const int grid = std::min(ntiles, cu_count());
-  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, FL_GEMM_PP_BK, FL_GEMM_PP_NS>), dim3(grid), dim3(512),
-                     0, s, p, ntiles);
+  // SwiGLU's output staging area (8 waves x FL_GEMM_PP_SPREAD KB) takes the
+  // LDS of one stage when it exceeds the 32 KB that four stages leave.
+  constexpr int NS = EPI == EPI_SWIGLU && FL_GEMM_PP_SPREAD > 4 ? FL_GEMM_PP_NS - 1 : FL_GEMM_PP_NS;
+  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, FL_GEMM_PP_BK, NS>), dim3(grid), dim3(512), 0,
+                     s, p, ntiles);
   return hipGetLastError();
 }
 
@@ -1426,6 +1542,8 @@ int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bia
   if (!FL_GEMM_PP || (dtype != F16 && dtype != BF16)) return -1;
   if (N <= 0 || K <= 0 || N % 256 || K % FL_GEMM_PP_BK) return -1;
   if (!pp_epilogue_ok(epi_kind, math)) return -1;
+  // SwiGLU stores a tile's staged row blocks over the next tile's K steps.
+  if (epi_kind == EPI_SWIGLU && K / FL_GEMM_PP_BK < 8) return -1;
   if (epi_kind == EPI_ROPE) return has_bias ? -1 : PACK_ROPE;
   return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
 }

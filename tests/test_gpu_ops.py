@@ -128,6 +128,30 @@ def test_gemm_16bit_many_tiles(ctx, fl, m, k, n):
     close(got[rows], want, 2 * ulp * np.abs(want).max() + 1e-3, 2 * ulp)
 
 
+@pytest.mark.parametrize("m,bias", [(65636, False), (300, True)])
+def test_linear_swiglu_staged_epilogue(ctx, fl, orc, m, bias):
+    # The SwiGLU epilogue stages each finished tile's outputs in LDS and stores
+    # them over the next tile's K steps: many tiles per workgroup with a
+    # ragged last row block, and a bias, against float64 on the rounded
+    # operands (rows sampled over every row block plus the last ones).
+    k, n = 768, 2048
+    rng = np.random.default_rng(m)
+    x = (rng.standard_normal((m, k)) * 0.5).astype(np.float32)
+    w = (rng.standard_normal((k, n)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32) if bias else None
+    dx, dw = ctx.tensor(x, fl.F16), ctx.tensor(w, fl.F16)
+    db = ctx.tensor(b, fl.F16) if bias else None
+    got = ctx.linear(dx, dw, db, act=4, math=fl.MATH_EXACT).numpy()
+    rows = np.unique(np.concatenate([np.arange(0, m, 89), np.arange(max(0, m - 40), m)]))
+    y = f16(x)[rows].astype(np.float64) @ f16(w).astype(np.float64)
+    if bias:
+        y += f16(b).astype(np.float64)
+    h = n // 2
+    want = y[:, :h] / (1 + np.exp(-y[:, :h])) * y[:, h:]
+    ulp = 2 ** -10
+    close(got[rows], want, 4 * ulp * np.abs(want).max() + 1e-3, 4 * ulp)
+
+
 def exact_activation(orc, x, w, b, act):
     """FL_MATH_EXACT reference: the oracle's product, then the activation in
     float64 (the oracle's own GELU is the reference's TanhFast formula, which
