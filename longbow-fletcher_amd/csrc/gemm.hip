@@ -501,407 +501,6 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_lds_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Direct-LDS 16-bit GEMM on 32x32x16 MFMAs (gfx950 issues these at twice the
-// flop rate of 16x16x32).  Operand fragments: lane l holds 8 consecutive k of
-// row (l % 32); lanes 0-31 and 32-63 take the two 8-wide k chunks of a
-// 16-deep step.  Accumulator: lane l holds token column (l % 32) and output
-// features 8j + 4(l / 32) + i (register 4j + i), i.e. four runs of four
-// consecutive features, so the RoPE pair (d, d + 32) sits in registers 4j + i
-// of adjacent 32-feature tiles and the SwiGLU (gate, up) pair in registers
-// 4j + i and 4(j + 2) + i of one tile (weights packed in 16-column blocks).
-// ---------------------------------------------------------------------------
-template <typename T> struct Mfma32;
-template <> struct Mfma32<_Float16> {
-  __device__ static inline void mma(float16_t& c, const u32x4_t& a, const u32x4_t& b) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
-                                               __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
-  }
-};
-template <> struct Mfma32<__bf16> {
-  __device__ static inline void mma(float16_t& c, const u32x4_t& a, const u32x4_t& b) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  }
-};
-
-template <typename T, int BM, int BN, int BK, int WM, int WN, int EPI, int MATH, int SWZ_SHIFT>
-__global__ void __launch_bounds__(WM* WN * 64, 2) gemm_lds32_kernel(GemmParams p) {
-  constexpr int NW = WM * WN;
-  constexpr int ROWB = BK * 2, CPR = BK / 8, RPI = 64 / CPR;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, FN = WTN / 32;
-  constexpr int A_INS = BM / RPI / NW, B_INS = BN / RPI / NW;
-  static_assert(BK == 32 || BK == 64, "BK 32 or 64");
-  static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile/wave mismatch");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "32x32 tiles");
-  static_assert(EPI != EPI_ROPE || WTN % 64 == 0, "RoPE needs whole 64-wide heads per wave");
-  __shared__ __attribute__((aligned(1024))) char lds0[(BM + BN) * ROWB];
-  __shared__ __attribute__((aligned(1024))) char lds1[(BM + BN) * ROWB];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
-  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  constexpr int GROUP_M = 8;
-  const int per_group = GROUP_M * num_n;
-  const int g = L / per_group;
-  const int first_m = g * GROUP_M;
-  const int gsize = min(num_m - first_m, GROUP_M);
-  const int r = L - g * per_group;
-  const int m0 = (first_m + r % gsize) * BM;
-  const int n0 = (r / gsize) * BN;
-  const int M = p.M;
-
-  const char* abase = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
-  const char* bbase = (const char*)p.B + (size_t)n0 * p.ldb * sizeof(T);
-  uint32_t aoff[A_INS], boff[B_INS];
-#pragma unroll
-  for (int i = 0; i < A_INS; ++i) {
-    const int row = (wave * A_INS + i) * RPI + lane / CPR;
-    const int c = (lane % CPR) ^ lds_swz<SWZ_SHIFT, CPR>(row);
-    const int rr = min(row, M - 1 - m0);
-    aoff[i] = (uint32_t)(rr * p.lda + c * 8) * (uint32_t)sizeof(T);
-  }
-#pragma unroll
-  for (int i = 0; i < B_INS; ++i) {
-    const int row = (wave * B_INS + i) * RPI + lane / CPR;
-    const int c = (lane % CPR) ^ lds_swz<SWZ_SHIFT, CPR>(row);
-    boff[i] = (uint32_t)(row * p.ldb + c * 8) * (uint32_t)sizeof(T);
-  }
-  auto issue = [&](char* stage, int k0) {
-    const char* ak = abase + (size_t)k0 * sizeof(T);
-    const char* bk = bbase + (size_t)k0 * sizeof(T);
-#pragma unroll
-    for (int i = 0; i < A_INS; ++i)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(ak + aoff[i]),
-          (__attribute__((address_space(3))) void*)(stage + (wave * A_INS + i) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < B_INS; ++i)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(bk + boff[i]),
-          (__attribute__((address_space(3))) void*)(stage + BM * ROWB + (wave * B_INS + i) * 1024),
-          16, 0, 0);
-  };
-
-  const int fr = lane & 31, fh = lane >> 5;
-  const int swz = lds_swz<SWZ_SHIFT, CPR>(fr);
-  const int a_row0 = (wm * WTM + fr) * ROWB;
-  const int b_row0 = BM * ROWB + (wn * WTN + fr) * ROWB;
-
-  float16_t acc[FN][TM];
-#pragma unroll
-  for (int f = 0; f < FN; ++f)
-#pragma unroll
-    for (int t = 0; t < TM; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.f;
-
-  auto compute = [&](const char* stage) {
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int co = ((ks * 2 + fh) ^ swz) << 4;
-      u32x4_t fa[TM], fb[FN];
-#pragma unroll
-      for (int t = 0; t < TM; ++t) fa[t] = *(const u32x4_t*)(stage + a_row0 + t * 32 * ROWB + co);
-#pragma unroll
-      for (int f = 0; f < FN; ++f) fb[f] = *(const u32x4_t*)(stage + b_row0 + f * 32 * ROWB + co);
-#pragma unroll
-      for (int f = 0; f < FN; ++f)
-#pragma unroll
-        for (int t = 0; t < TM; ++t) Mfma32<T>::mma(acc[f][t], fb[f], fa[t]);
-    }
-  };
-
-  // K is a multiple of 2*BK (checked on the host): stages alternate without a
-  // mid-loop exit; the last iteration re-fetches slice 0 into the idle stage
-  // (in bounds, never read) so the loop body stays branch-free.
-  const int nk = p.K / BK;
-  issue(lds0, 0);
-  for (int kt = 0; kt < nk; kt += 2) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue(lds1, (kt + 1) * BK);
-    compute(lds0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue(lds0, (kt + 2 < nk ? kt + 2 : 0) * BK);
-    compute(lds1);
-  }
-  // No DMA may still target this workgroup's LDS when it exits.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  T* C = (T*)p.C;
-  const int nbase = n0 + wn * WTN;
-  const float* bias = p.epi.bias;
-#pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    const int m = m0 + wm * WTM + t * 32 + fr;
-    if (m >= M) continue;
-    T* crow = C + (size_t)m * p.ldc;
-    if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-      for (int f = 0; f < FN; ++f) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int ng = nbase + f * 32 + 8 * j + 4 * fh;  // gate column (packed order)
-          float4_t o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float gt = acc[f][t][4 * j + i], up = acc[f][t][4 * (j + 2) + i];
-            if (bias) {
-              gt += bias[ng + i];
-              up += bias[ng + 16 + i];
-            }
-            o[i] = silu_m<MATH>(gt) * up;
-          }
-          store4<T>(crow + (nbase + f * 32) / 2 + 8 * j + 4 * fh, o);
-        }
-      }
-    } else if constexpr (EPI == EPI_ROPE) {
-#pragma unroll
-      for (int h = 0; h < FN / 2; ++h) {
-        const int hb = nbase + h * 64;
-        float16_t lo = acc[2 * h][t], hi = acc[2 * h + 1][t];
-        if (bias) {
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            const int d = 8 * (rr / 4) + 4 * fh + (rr % 4);
-            lo[rr] += bias[hb + d];
-            hi[rr] += bias[hb + 32 + d];
-          }
-        }
-        if (hb < p.epi.rope_cols) {
-#pragma clang fp contract(off)
-          const float2* cs = p.epi.rope_cs + (size_t)p.epi.pos[m] * 32;
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            const float2 c = cs[8 * (rr / 4) + 4 * fh + (rr % 4)];
-            const float x1 = lo[rr], x2 = hi[rr];
-            lo[rr] = x1 * c.x - x2 * c.y;
-            hi[rr] = x1 * c.y + x2 * c.x;
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          store4<T>(crow + hb + 8 * j + 4 * fh,
-                    float4_t{lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]});
-          store4<T>(crow + hb + 32 + 8 * j + 4 * fh,
-                    float4_t{hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]});
-        }
-      }
-    } else {
-#pragma unroll
-      for (int f = 0; f < FN; ++f) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = nbase + f * 32 + 8 * j + 4 * fh;
-          float4_t v = {acc[f][t][4 * j], acc[f][t][4 * j + 1], acc[f][t][4 * j + 2],
-                        acc[f][t][4 * j + 3]};
-          if (bias) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] += bias[n + i];
-          }
-          store4<T>(crow + n, act4<EPI, MATH>(v));
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Persistent variant of the direct-LDS GEMM: the grid holds two workgroups
-// per CU and each walks tiles L = round * grid + xcd_remap(block), streaming
-// the K slices of consecutive tiles through the same two LDS stages.  The
-// first slice of the next tile is in flight while the current tile runs its
-// epilogue, so neither the prologue latency nor the epilogue stalls the
-// MFMA pipe.  BK = 32 (64-byte LDS rows, 4 chunks, swizzle (row >> 1) & 3).
-// ---------------------------------------------------------------------------
-template <typename T, int EPI, int MATH, bool BIAS = true>
-__device__ __attribute__((always_inline)) inline void tile_epilogue(const GemmParams& p, const float4_t (&acc)[4][8], int m0,
-                                     int nbase, int wm_off, int lane) {
-  constexpr int TM = 8, FN = 4;
-  // Opaque copy of the lane id: stops lane-dependent epilogue addresses from
-  // being hoisted out of a persistent kernel's tile loop into registers.
-  asm volatile("" : "+v"(lane));
-  T* C = (T*)p.C;
-  const int lrow = lane & 15, lgrp = lane >> 4;
-  const float* bias = BIAS ? p.epi.bias : nullptr;
-#pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    const int m = m0 + wm_off + t * 16 + lrow;
-    if (m >= p.M) continue;
-    T* crow = C + (size_t)m * p.ldc;
-    if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-      for (int j = 0; j < FN / 2; ++j) {
-        const int ng = nbase + 2 * j * 16 + lgrp * 4;
-        float4_t gt = acc[2 * j][t], up = acc[2 * j + 1][t];
-        if (bias) {
-          gt += *(const float4_t*)(bias + ng);
-          up += *(const float4_t*)(bias + ng + 16);
-        }
-        float4_t o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = silu_m<MATH>(gt[i]) * up[i];
-        store4<T>(crow + nbase / 2 + j * 16 + lgrp * 4, o);
-      }
-    } else if constexpr (EPI == EPI_ROPE) {
-      const int hb = nbase;
-      float4_t v[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        v[q] = acc[q][t];
-        if (bias) v[q] += *(const float4_t*)(bias + hb + q * 16 + lgrp * 4);
-      }
-      if (hb < p.epi.rope_cols) {
-#pragma clang fp contract(off)
-        const float2* cs = p.epi.rope_cs + (size_t)p.epi.pos[m] * 32;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float2 c = cs[q * 16 + lgrp * 4 + i];
-            const float x1 = v[q][i], x2 = v[q + 2][i];
-            v[q][i] = x1 * c.x - x2 * c.y;
-            v[q + 2][i] = x1 * c.y + x2 * c.x;
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) store4<T>(crow + hb + q * 16 + lgrp * 4, v[q]);
-    } else {
-#pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        const int n = nbase + f * 16 + lgrp * 4;
-        float4_t v = acc[f][t];
-        if (bias) v += *(const float4_t*)(bias + n);
-        store4<T>(crow + n, act4<EPI, MATH>(v));
-      }
-    }
-    // One row block at a time: hoisting every block's table loads would
-    // need more registers than the accumulators leave.
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-template <typename T, int EPI, int MATH>
-__global__ void __launch_bounds__(256, 2) gemm_persist_kernel(GemmParams p, int ntiles) {
-  constexpr int BM = 256, BN = 128, BK = 32, WN = 2;
-  constexpr int ROWB = 64, CPR = 4, RPI = 16;
-  constexpr int WTM = 128, WTN = 64, TM = 8, FN = 4;
-  constexpr int A_INS = BM / RPI / 4, B_INS = BN / RPI / 4;  // 4 and 2 per wave
-  constexpr int GROUP_M = 8;
-  __shared__ __attribute__((aligned(1024))) char lds0[(BM + BN) * ROWB];
-  __shared__ __attribute__((aligned(1024))) char lds1[(BM + BN) * ROWB];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int G = (int)gridDim.x;
-  const int me = xcd_remap((int)blockIdx.x, G);
-  const int my_tiles = me < ntiles ? (ntiles - me + G - 1) / G : 0;
-  const int nk = p.K / BK;
-  const int total = my_tiles * nk;
-  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
-  const int per_group = GROUP_M * num_n;
-  auto coords = [&](int i, int& m0, int& n0) {
-    const int L = i * G + me;
-    const int g = L / per_group;
-    const int first_m = g * GROUP_M;
-    const int gsize = min(num_m - first_m, GROUP_M);
-    const int r = L - g * per_group;
-    m0 = (first_m + r % gsize) * BM;
-    n0 = (r / gsize) * BN;
-  };
-
-  // Per-lane load geometry (row within the tile, swizzled chunk).
-  int arow[A_INS], brow[B_INS], ac[A_INS], bc[B_INS];
-#pragma unroll
-  for (int i = 0; i < A_INS; ++i) {
-    arow[i] = (wave * A_INS + i) * RPI + lane / CPR;
-    ac[i] = ((lane % CPR) ^ ((arow[i] >> 1) & 3)) * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < B_INS; ++i) {
-    brow[i] = (wave * B_INS + i) * RPI + lane / CPR;
-    bc[i] = ((lane % CPR) ^ ((brow[i] >> 1) & 3)) * 8;
-  }
-  // Issues the loads of global slice gi (gi >= total re-fetches slice 0: in
-  // bounds, never read) into `stage`.
-  auto issue = [&](char* stage, int gi) {
-    if (gi >= total) gi = 0;
-    const int ti = gi / nk, k0 = (gi - ti * nk) * BK;
-    int m0, n0;
-    coords(ti, m0, n0);
-    const T* A = (const T*)p.A + k0;
-    const T* B = (const T*)p.B + (size_t)n0 * p.ldb + k0;
-    const int lim = p.M - 1 - m0;
-#pragma unroll
-    for (int i = 0; i < A_INS; ++i) {
-      const T* src = A + (size_t)(m0 + min(arow[i], lim)) * p.lda + ac[i];
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(stage + (wave * A_INS + i) * 1024),
-                                       16, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < B_INS; ++i) {
-      const T* src = B + (size_t)brow[i] * p.ldb + bc[i];
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(stage + BM * ROWB + (wave * B_INS + i) * 1024),
-                                       16, 0, 0);
-    }
-  };
-
-  const int fr = lane & 15, fg = lane >> 4;
-  const int co = (fg ^ ((fr >> 1) & 3)) << 4;
-  const int a_off = (wm * WTM + fr) * ROWB + co;
-  const int b_off = BM * ROWB + (wn * WTN + fr) * ROWB + co;
-
-  float4_t acc[FN][TM];
-  auto zero = [&]() {
-#pragma unroll
-    for (int f = 0; f < FN; ++f)
-#pragma unroll
-      for (int t = 0; t < TM; ++t) acc[f][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  };
-  auto compute = [&](const char* stage) {
-    u32x4_t fa[TM], fb[FN];
-#pragma unroll
-    for (int t = 0; t < TM; ++t) fa[t] = *(const u32x4_t*)(stage + a_off + t * 16 * ROWB);
-#pragma unroll
-    for (int f = 0; f < FN; ++f) fb[f] = *(const u32x4_t*)(stage + b_off + f * 16 * ROWB);
-#pragma unroll
-    for (int f = 0; f < FN; ++f)
-#pragma unroll
-      for (int t = 0; t < TM; ++t) Mfma<T>::mma(acc[f][t], fb[f], fa[t]);
-  };
-
-  zero();
-  if (total == 0) return;
-  issue(lds0, 0);
-  // nk is even (K % 64 == 0, checked on the host): slices alternate stages
-  // and a tile always ends on the second half of an iteration.
-  for (int gi = 0; gi < total; gi += 2) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue(lds1, gi + 1);
-    compute(lds0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue(lds0, gi + 2);
-    compute(lds1);
-    const int ti = (gi + 1) / nk;
-    if (gi + 2 - ti * nk == nk) {
-      int m0, n0;
-      coords(ti, m0, n0);
-      tile_epilogue<T, EPI, MATH>(p, acc, m0, n0 + wn * WTN, wm * WTM, lane);
-      zero();
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-// ---------------------------------------------------------------------------
 // Ping-pong epilogue.  B (and the bias) are packed so that the 16 values a
 // lane holds for one row block are adjacent outputs (PackLayout), so each
 // lane stores 16 bytes at a time.  The bias is read in packed order.
@@ -1377,35 +976,21 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
 }
 
 // ---------------------------------------------------------------------------
-// Tile configurations.  16-bit: 256x256 tiles of 4 waves x (128x128) when
-// N % 256 == 0 (4 MFMAs per 16-byte LDS fragment read, 144 KB of LDS double
-// buffered, one workgroup per CU), else 256x128 tiles of 4 x (128x64).
+// Tile configurations of the 4-wave kernels, which take what the ping-pong
+// kernel does not (fp32, GELU/tanh epilogues, N % 256 != 0): 16-bit 256x128
+// tiles of 4 waves x (128x64); fp32 128x64 tiles of 2 waves.
 // ---------------------------------------------------------------------------
-struct Cfg256x256 { static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2; };
 struct Cfg256x128 { static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2; };
-struct Cfg128x128 { static constexpr int BM = 128, BN = 128, BK = 64, WM = 2, WN = 2; };
 // Direct-LDS 16-bit GEMM defaults: 256x128 tiles, BK = 32, two LDS stages
 // (48 KB, so two workgroups share a CU), chunk swizzle (row >> 1) & 3.
 #ifndef FL_GEMM_SWZ
 #define FL_GEMM_SWZ 1
-#endif
-#ifndef FL_GEMM_LDS_CFG
-#define FL_GEMM_LDS_CFG 1
 #endif
 #ifndef FL_GEMM_STAGES
 #define FL_GEMM_STAGES 2
 #endif
 #ifndef FL_GEMM_BK
 #define FL_GEMM_BK 32
-#endif
-#ifndef FL_GEMM_MFMA32
-#define FL_GEMM_MFMA32 0
-#endif
-#ifndef FL_GEMM_PERSIST
-#define FL_GEMM_PERSIST 0
-#endif
-#ifndef FL_GEMM_NT_256
-#define FL_GEMM_NT_256 0
 #endif
 struct CfgF32 { static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1; };
 
@@ -1434,14 +1019,6 @@ static int cu_count() {
   return counts[dev];
 }
 
-template <typename T, int EPI, int MATH>
-static hipError_t launch_persist(const GemmParams& p, hipStream_t s) {
-  const int ntiles = ((p.M + 255) / 256) * (p.N / 128);
-  const int grid = std::min(ntiles, 2 * cu_count());
-  hipLaunchKernelGGL((gemm_persist_kernel<T, EPI, MATH>), dim3(grid), dim3(256), 0, s, p, ntiles);
-  return hipGetLastError();
-}
-
 // Epilogues the ping-pong kernel is built for.  The others (GELU, tanh, the
 // reference-formula SiLU) need more registers than it leaves next to its
 // accumulators and take the 4-wave kernels; so does RoPE with a bias.
@@ -1458,17 +1035,6 @@ static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   constexpr int NS = EPI == EPI_SWIGLU && FL_GEMM_PP_SPREAD > 4 ? FL_GEMM_PP_NS - 1 : FL_GEMM_PP_NS;
   hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, FL_GEMM_PP_BK, NS>), dim3(grid), dim3(512), 0,
                      s, p, ntiles);
-  return hipGetLastError();
-}
-
-template <typename T, typename C, int EPI, int MATH>
-static hipError_t launch_lds32(const GemmParams& p, hipStream_t s) {
-  const int num_m = (p.M + C::BM - 1) / C::BM;
-  const int num_n = p.N / C::BN;
-  dim3 grid(num_m * num_n), block(C::WM * C::WN * 64);
-  hipLaunchKernelGGL((gemm_lds32_kernel<T, C::BM, C::BN, FL_GEMM_BK, C::WM, C::WN, EPI, MATH,
-                                        FL_GEMM_SWZ>),
-                     grid, block, 0, s, p);
   return hipGetLastError();
 }
 
@@ -1493,22 +1059,7 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
       if constexpr (pp_epilogue_ok(EPI, MATH)) return launch_pp<T, EPI, MATH>(p, s);
       return hipErrorInvalidValue;
     }
-#if FL_GEMM_MFMA32 == 1
-    if (p.K % (2 * FL_GEMM_BK) == 0) return launch_lds32<T, Cfg256x128, EPI, MATH>(p, s);
-#elif FL_GEMM_MFMA32 == 2
-    if (p.K % (2 * FL_GEMM_BK) == 0) return launch_lds32<T, Cfg128x128, EPI, MATH>(p, s);
-#endif
-#if FL_GEMM_PERSIST
-    if (p.K % 64 == 0) return launch_persist<T, EPI, MATH>(p, s);
-#endif
-#if FL_GEMM_LDS_CFG == 2
-    if (p.N % 256 == 0 && p.K % 128 == 0) return launch_lds<T, Cfg256x256, EPI, MATH>(p, s);
-#elif FL_GEMM_LDS_CFG == 3
-    if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg128x128, EPI, MATH>(p, s);
-#elif FL_GEMM_LDS_CFG == 1
     if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
-#endif
-    if (p.N % 256 == 0 && FL_GEMM_NT_256) return launch_cfg<T, Cfg256x256, EPI, MATH>(p, s);
     return launch_cfg<T, Cfg256x128, EPI, MATH>(p, s);
   }
 }
