@@ -11,6 +11,7 @@
 // features of one token: stores are 8/16-byte vectors and the RoPE pair
 // (j, j+32) and the SwiGLU (gate, up) pair land in the same lane.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -29,11 +30,17 @@
 #ifndef FL_GEMM_PP_SPREAD
 #define FL_GEMM_PP_SPREAD 8
 #endif
+#ifndef FL_GEMM_W4
+#define FL_GEMM_W4 1
+#endif
 #ifndef FL_GEMM_PP_GROUP_M
 #define FL_GEMM_PP_GROUP_M 8
 #endif
 
 namespace fl {
+
+// Register-level K steps and accumulator reads of gemm_w4_kernel.
+#include "gemm_w4.inc"
 
 template <typename T> struct Mfma;
 template <> struct Mfma<_Float16> {
@@ -518,6 +525,76 @@ __device__ inline void store8(T* dst, float4_t a, float4_t b) {
   }
 }
 
+// One 16-row block of a 64-feature group: v[f] is accumulator tile f of the
+// group for token rows m - (lane & 15) .. +15 (lane holds row m); nbase is
+// the group's first (packed) output column.
+template <typename T, int EPI, int MATH, bool BIAS>
+__device__ __attribute__((always_inline)) inline void pp_epilogue_block(const GemmParams& p,
+                                                                        float4_t (&v)[4], int m,
+                                                                        int nbase, int lane) {
+  T* C = (T*)p.C;
+  const int g = lane >> 4;
+  // Rows past M are computed on row M-1's inputs and not stored.
+  const bool ok = m < p.M;
+  const int mc = ok ? m : p.M - 1;
+  T* crow = C + (size_t)mc * p.ldc;
+  if constexpr (BIAS) {
+    if (p.epi.bias) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) v[f] += *(const float4_t*)(p.epi.bias + nbase + f * 16 + g * 4);
+    }
+  }
+  if constexpr (EPI == EPI_SWIGLU) {
+    // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
+    float4_t o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(v[2 * h][i]) * v[2 * h + 1][i];
+    }
+    if (ok) store8<T>(crow + nbase / 2 + g * 8, o[0], o[1]);
+  } else if constexpr (EPI == EPI_ROPE) {
+    // PACK_ROPE: tiles 0 / 1 hold dims 8g+i / 8g+4+i of the head, tiles
+    // 2 / 3 their rotate-half partners 32+8g+i / 32+8g+4+i.
+    if (nbase < p.epi.rope_cols) {
+#pragma clang fp contract(off)
+      const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
+      const float4_t* cs = (const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4_t c = cs[f * 2 + h];  // (cos, sin) of dims 8g + 4f + 2h, +1
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int i = 2 * h + e;
+            const float x1 = v[f][i], x2 = v[f + 2][i];
+            const float co = c[2 * e], si = c[2 * e + 1];
+            v[f][i] = x1 * co - x2 * si;
+            v[f + 2][i] = x1 * si + x2 * co;
+          }
+        }
+      }
+    }
+    if (ok) {
+      store8<T>(crow + nbase + g * 8, v[0], v[1]);
+      store8<T>(crow + nbase + 32 + g * 8, v[2], v[3]);
+    }
+  } else {
+    // PACK_LANE16: tile f holds outputs 16g+4f+i.
+#pragma unroll
+    for (int f = 0; f < 4; ++f) v[f] = act4<EPI, MATH>(v[f]);
+    if (nbase < p.epi.q_cols) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) v[f] *= p.epi.q_scale;
+    }
+    if (ok) {
+      store8<T>(crow + nbase + g * 16, v[0], v[1]);
+      store8<T>(crow + nbase + g * 16 + 8, v[2], v[3]);
+    }
+  }
+}
+
 template <typename T, int EPI, int MATH, bool BIAS>
 __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmParams& p,
                                                                   const float4_t (&acc)[4][8],
@@ -527,75 +604,10 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmPara
   // Opaque copy of the lane id: stops lane-dependent epilogue addresses from
   // being hoisted out of the tile loop into registers.
   asm volatile("" : "+v"(lane));
-  T* C = (T*)p.C;
-  const int lrow = lane & 15, g = lane >> 4;
-  const float* bias = BIAS ? p.epi.bias : nullptr;
-  auto biased = [&](int f, int t) __attribute__((always_inline)) {
-    float4_t v = acc[f][t];
-    if (bias) v += *(const float4_t*)(bias + nbase + f * 16 + g * 4);
-    return v;
-  };
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
-    // Rows past M are computed on row M-1's inputs and not stored.
-    const int m = m0 + wm_off + t * 16 + lrow;
-    const bool ok = m < p.M;
-    const int mc = ok ? m : p.M - 1;
-    T* crow = C + (size_t)mc * p.ldc;
-    if constexpr (EPI == EPI_SWIGLU) {
-      // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
-      float4_t o[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float4_t gt = biased(2 * h, t), up = biased(2 * h + 1, t);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(gt[i]) * up[i];
-      }
-      if (ok) store8<T>(crow + nbase / 2 + g * 8, o[0], o[1]);
-    } else if constexpr (EPI == EPI_ROPE) {
-      // PACK_ROPE: tiles 0 / 1 hold dims 8g+i / 8g+4+i of the head, tiles
-      // 2 / 3 their rotate-half partners 32+8g+i / 32+8g+4+i.
-      float4_t v[4];
-#pragma unroll
-      for (int f = 0; f < 4; ++f) v[f] = biased(f, t);
-      if (nbase < p.epi.rope_cols) {
-#pragma clang fp contract(off)
-        const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
-        const float4_t* cs = (const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8);
-#pragma unroll
-        for (int f = 0; f < 2; ++f) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float4_t c = cs[f * 2 + h];  // (cos, sin) of dims 8g + 4f + 2h, +1
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int i = 2 * h + e;
-              const float x1 = v[f][i], x2 = v[f + 2][i];
-              const float co = c[2 * e], si = c[2 * e + 1];
-              v[f][i] = x1 * co - x2 * si;
-              v[f + 2][i] = x1 * si + x2 * co;
-            }
-          }
-        }
-      }
-      if (ok) {
-        store8<T>(crow + nbase + g * 8, v[0], v[1]);
-        store8<T>(crow + nbase + 32 + g * 8, v[2], v[3]);
-      }
-    } else {
-      // PACK_LANE16: tile f holds outputs 16g+4f+i.
-      float4_t v[4];
-#pragma unroll
-      for (int f = 0; f < 4; ++f) v[f] = act4<EPI, MATH>(biased(f, t));
-      if (nbase < p.epi.q_cols) {
-#pragma unroll
-        for (int f = 0; f < 4; ++f) v[f] *= p.epi.q_scale;
-      }
-      if (ok) {
-        store8<T>(crow + nbase + g * 16, v[0], v[1]);
-        store8<T>(crow + nbase + g * 16 + 8, v[2], v[3]);
-      }
-    }
+    float4_t v[4] = {acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
+    pp_epilogue_block<T, EPI, MATH, BIAS>(p, v, m0 + wm_off + t * 16 + (lane & 15), nbase, lane);
     // One row block at a time: hoisting every block's table loads would
     // need more registers than the accumulators leave.
     __builtin_amdgcn_sched_barrier(0);
@@ -736,22 +748,29 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   // 16-byte chunk l%CPR of row l/CPR of each 1 KB load, holding global chunk
   // (l%CPR) ^ swz(row).  Activation rows past M re-read row M-1 (never
   // stored).
-  const char* gsrc = grp == 0 ? (const char*)p.A : (const char*)p.B;
-  const int ld = grp == 0 ? p.lda : p.ldb;
+  // The weights are stored tiled (tiled_offset): a stage's weight half is
+  // one contiguous 16 KB block, already in LDS order.
+  static_assert(BK == 32, "tiled weights hold 32-deep K slices");
   const int lrow = lane / CPR, lcol = lane % CPR;
+  const size_t kstride = grp == 0 ? BK * sizeof(T) : (size_t)BN * BK * sizeof(T);
   uint32_t off[NLD];
   const char* gbase = nullptr;
   auto load_tile = [&](int ti) __attribute__((always_inline)) {
     int m0, n0;
     coords(ti, m0, n0);
-    const int r0 = grp == 0 ? m0 : n0;
-    const int lim = grp == 0 ? p.M - 1 - m0 : BN - 1;
-    gbase = gsrc + (size_t)r0 * ld * sizeof(T);
+    if (grp == 0) {
+      const int lim = p.M - 1 - m0;
+      gbase = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) {
-      const int row = (wn * NLD + j) * RPL + lrow;
-      const int c = lcol ^ pp_swz<CPR>(row);
-      off[j] = (uint32_t)(min(row, lim) * ld + c * 8) * (uint32_t)sizeof(T);
+      for (int j = 0; j < NLD; ++j) {
+        const int row = (wn * NLD + j) * RPL + lrow;
+        const int c = lcol ^ pp_swz<CPR>(row);
+        off[j] = (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
+      }
+    } else {
+      gbase = (const char*)p.B + (size_t)(n0 / BN) * nk * kstride;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) off[j] = (uint32_t)((wn * NLD + j) * 1024 + lane * 16);
     }
   };
   // DMA cursor: the step that the next issue loads.  Past the last step it
@@ -760,7 +779,7 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   // the wait counts stay uniform.
   int ld_tile = 0, ld_k = 0;
   auto issue_one = [&](char* stage, int j) __attribute__((always_inline)) {
-    const char* src = gbase + (size_t)ld_k * BK * sizeof(T);
+    const char* src = gbase + (size_t)ld_k * kstride;
     char* dst = stage + grp * (BM * ROWB) + wn * NLD * 1024;
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + off[j]),
                                      (__attribute__((address_space(3))) void*)(dst + j * 1024), 16,
@@ -976,6 +995,220 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
 }
 
 // ---------------------------------------------------------------------------
+// Four-wave 16-bit GEMM: 256x256 tiles, one wave per SIMD, each wave owning a
+// 128x128 output block (64 accumulator tiles in AGPRs), NS LDS stages of
+// 32-deep K slices in the ping-pong kernel's layout (same packed weights,
+// same epilogues).  Against the ping-pong kernel's 128x64 wave tiles this
+// reads a third fewer bytes from LDS per MFMA and needs one barrier per K
+// step instead of two; the price is that nothing hides the epilogue.
+//
+// A K step is written out as volatile asm: 64 MFMAs, interleaved with the 16
+// LDS fragment reads of the next step (into the other register set) and the
+// wave's 8 DMA loads of step s+NS-1, in a fixed order the compiler cannot
+// rearrange.  The step ends with the DMA wait for step s+2, the fragment
+// wait and one barrier.
+//
+// Step s reads stage (s+1)%NS and loads stage (s+NS-1)%NS = (s-1)%NS, which
+// was last read in step s-2, before the barrier that ended it.  At the end of
+// step s each wave waits until its own loads of step s+2 have landed; after
+// the barrier every wave's have.
+// ---------------------------------------------------------------------------
+// The K-step blocks set m0 (the LDS address of DMA loads) themselves; the
+// compiler emits no m0 use of its own in this kernel.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One 1 KB DMA load outside the K-step blocks (prologue): 64 lanes x 16
+// bytes from gsrc + voff into LDS at lds_dst.
+__device__ __attribute__((always_inline)) inline void w4_dma(uint32_t lds_dst, uint32_t voff,
+                                                             const void* gsrc) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2" ::"s"(lds_dst),
+      "v"(voff), "s"(gsrc)
+      : "memory", "m0");
+}
+
+template <typename T, int EPI, int MATH, int NS>
+__global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) {
+  constexpr int BM = 256, BN = 256, BK = 32, ROWB = 64;
+  constexpr int STAGE = (BM + BN) * ROWB;     // 32 KB
+  constexpr int NLD = 8;                      // 1 KB loads per wave per step
+  constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
+  constexpr bool F16T = Elem<T>::dtype == F16;
+  static_assert(NS == 4, "the K loop runs in groups of four steps, one per stage");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int G = (int)gridDim.x;
+  const int me = xcd_remap((int)blockIdx.x, G);
+  const int my_tiles = me < ntiles ? (ntiles - 1 - me) / G + 1 : 0;
+  if (my_tiles == 0) return;
+  const bool chunked = (ntiles % G == 0) && (G % 8 == 0);
+  const int per = G / 8;
+  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
+  const int per_group = GROUP_M * num_n;
+  auto coords = [&](int i, int& m0, int& n0) __attribute__((always_inline)) {
+    const int L = chunked ? (me / per) * (my_tiles * per) + i * per + (me % per) : i * G + me;
+    const int g = L / per_group;
+    const int first_m = g * GROUP_M;
+    const int gsize = min(num_m - first_m, GROUP_M);
+    const int r = L - g * per_group;
+    m0 = (first_m + r % gsize) * BM;
+    n0 = (r / gsize) * BN;
+  };
+  const int nk = p.K / BK;
+
+  // DMA geometry: wave w loads activation rows [64w, 64w+64) (loads 0-3) and
+  // weight rows [64w, 64w+64) (loads 4-7) of each stage, 16 rows x 64 bytes
+  // per load; lane l writes 16-byte chunk l%4 of row l/4, holding global
+  // chunk (l%4) ^ swz(row).  Activation rows past M re-read row M-1.  The
+  // weights are stored tiled (tiled_offset), so their loads are contiguous.
+  const int lrow = lane >> 2, lcol = lane & 3;
+  uint32_t off[NLD];
+  const char* ka = nullptr;  // DMA cursor: token / weight base of the next K slice to load
+  const char* kb = nullptr;
+  constexpr size_t KB_STEP = (size_t)BN * BK * sizeof(T);  // one tiled weight block
+  auto load_tile = [&](int ti) __attribute__((always_inline)) {
+    int m0, n0;
+    coords(ti, m0, n0);
+    ka = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
+    kb = (const char*)p.B + (size_t)(n0 / BN) * nk * KB_STEP;
+    const int lim = p.M - 1 - m0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wave * 64 + j * 16 + lrow;
+      const int c = lcol ^ pp_swz<4>(row);
+      off[j] = (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
+      off[4 + j] = (uint32_t)((wave * 4 + j) * 1024 + lane * 16);
+    }
+  };
+
+  // Fragment reads: A block t is rows 128*wm + 16t + (lane & 15), B block f
+  // rows 128*wn + 16f + (lane & 15), 16-byte k chunk lane >> 4 (swizzled).
+  const int fr = lane & 15, fg = lane >> 4;
+  const uint32_t co = (uint32_t)((fg ^ pp_swz<4>(fr)) << 4);
+  const uint32_t rdA = lds0 + (uint32_t)((wm * 128 + fr) * ROWB) + co;
+  const uint32_t rdB = lds0 + (uint32_t)(BM * ROWB + (wn * 128 + fr) * ROWB) + co;
+  const uint32_t dma0 = lds0 + (uint32_t)wave * 4096;
+
+  // Prologue: steps 0 .. 2 into stages 0 .. 2; fragments of step 0 into
+  // register set 0.
+  load_tile(0);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+#pragma unroll
+    for (int j = 0; j < NLD; ++j)
+      w4_dma(dma0 + s * STAGE + (j < 4 ? j * 1024 : BM * ROWB + (j - 4) * 1024), off[j],
+             j < 4 ? ka : kb);
+    ka += BK * sizeof(T);
+    kb += KB_STEP;
+  }
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NLD * (NS - 3)) : "memory");
+  asm volatile(FL_W4_READ_0 ::"v"(rdA), "v"(rdB) : "memory", FL_W4_CLOBBER_V);
+
+  // K step j of a group of four (global step s = j mod 4, since every tile
+  // has a multiple of four steps): register set j % 2, reads stage (j+1)%4,
+  // loads the cursor's step into stage (j+3)%4, then advances the cursor.
+  // It first waits for its own loads of step s+1 (all but the last 8 loads
+  // issued), except in a tile's first step (Z): the wait before the
+  // epilogue already covered step s+1, and waiting here would also wait for
+  // the epilogue's stores.
+  auto kstep = [&](auto jc, auto zero) __attribute__((always_inline)) {
+    constexpr int J = decltype(jc)::value;
+    constexpr bool Z = decltype(zero)::value;
+    constexpr uint32_t RD = ((J + 1) % NS) * STAGE, DM = ((J + NS - 1) % NS) * STAGE;
+#define FL_W4_ARGS                                                                          \
+  ::"v"(rdA + RD), "v"(rdB + RD), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),        \
+      "v"(off[4]), "v"(off[5]), "v"(off[6]), "v"(off[7]), "s"(dma0 + DM), "s"(ka), "s"(kb),  \
+      "n"(Z ? 63 : NLD * (NS - 3))                                                         \
+  : "memory", "m0", "scc", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A
+    if constexpr (F16T) {
+      if constexpr (J % 2 == 0 && !Z) asm volatile(FL_W4_STEP_F16_0_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z) asm volatile(FL_W4_STEP_F16_0_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && !Z) asm volatile(FL_W4_STEP_F16_1_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z) asm volatile(FL_W4_STEP_F16_1_1 FL_W4_ARGS);
+    } else {
+      if constexpr (J % 2 == 0 && !Z) asm volatile(FL_W4_STEP_BF16_0_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z) asm volatile(FL_W4_STEP_BF16_0_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && !Z) asm volatile(FL_W4_STEP_BF16_1_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z) asm volatile(FL_W4_STEP_BF16_1_1 FL_W4_ARGS);
+    }
+#undef FL_W4_ARGS
+    ka += BK * sizeof(T);
+    kb += KB_STEP;
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  // Epilogue: accumulator tiles come out four at a time (one 16-row block
+  // of one 64-feature group), so the compiler's registers stay below v128.
+  auto epilogue = [&](int ti) __attribute__((always_inline)) {
+    int m0, n0;
+    coords(ti, m0, n0);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // The last MFMAs' results must be written before they are read.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    const int mrow = m0 + wm * 128 + (ln & 15);
+    auto block = [&](auto tc, auto hc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value, h = decltype(hc)::value;
+      float4_t v[4] = {W4Acc<(4 * h + 0) * 8 + t>::read(), W4Acc<(4 * h + 1) * 8 + t>::read(),
+                       W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
+      pp_epilogue_block<T, EPI, MATH, EPI != EPI_ROPE>(p, v, mrow + t * 16,
+                                                       n0 + wn * 128 + h * 64, ln);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto row = [&](auto tc) __attribute__((always_inline)) {
+      block(tc, I0{});
+      block(tc, I1{});
+    };
+    row(I0{});
+    row(I1{});
+    row(I2{});
+    row(I3{});
+    row(std::integral_constant<int, 4>{});
+    row(std::integral_constant<int, 5>{});
+    row(std::integral_constant<int, 6>{});
+    row(std::integral_constant<int, 7>{});
+    asm volatile("" ::: "memory");
+  };
+
+  // Per tile: group 0 (its first step multiplies into zero), groups 1 ..
+  // G-2, and the last group, whose steps 1-3 load the next tile's steps 0-2
+  // (past the last tile: its step 0 again, in bounds and never read).
+  const int G4 = nk / 4;
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    kstep(I0{}, std::true_type{});
+    kstep(I1{}, std::false_type{});
+    kstep(I2{}, std::false_type{});
+    kstep(I3{}, std::false_type{});
+    for (int g = 1; g < G4 - 1; ++g) {
+      kstep(I0{}, std::false_type{});
+      kstep(I1{}, std::false_type{});
+      kstep(I2{}, std::false_type{});
+      kstep(I3{}, std::false_type{});
+    }
+    kstep(I0{}, std::false_type{});
+    load_tile(ti + 1 < my_tiles ? ti + 1 : ti);
+    kstep(I1{}, std::false_type{});
+    kstep(I2{}, std::false_type{});
+    kstep(I3{}, std::false_type{});
+    // Step 1 of the next tile (loaded in step 2 of this group) has landed.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
+    epilogue(ti);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+#pragma clang diagnostic pop
+
+// ---------------------------------------------------------------------------
 // Tile configurations of the 4-wave kernels, which take what the ping-pong
 // kernel does not (fp32, GELU/tanh epilogues, N % 256 != 0): 16-bit 256x128
 // tiles of 4 waves x (128x64); fp32 128x64 tiles of 2 waves.
@@ -1038,6 +1271,15 @@ static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <typename T, int EPI, int MATH>
+static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
+  const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
+  const int grid = std::min(ntiles, cu_count());
+  hipLaunchKernelGGL((gemm_w4_kernel<T, EPI, MATH, 4>), dim3(grid), dim3(256), 0, s,
+                     p, ntiles);
+  return hipGetLastError();
+}
+
 template <typename T, typename C, int EPI, int MATH>
 static hipError_t launch_cfg(const GemmParams& p, hipStream_t s) {
   const int num_m = (p.M + C::BM - 1) / C::BM;
@@ -1056,7 +1298,9 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     // B packed for the ping-pong kernel (gemm_pp_layout) goes there; only the
     // epilogues it was built for reach this point with such a layout.
     if (p.epi.layout >= PACK_LANE16) {
-      if constexpr (pp_epilogue_ok(EPI, MATH)) return launch_pp<T, EPI, MATH>(p, s);
+      if constexpr (pp_epilogue_ok(EPI, MATH))
+        return FL_GEMM_W4 && p.K % 128 == 0 && p.K >= 256 ? launch_w4<T, EPI, MATH>(p, s)
+                                                         : launch_pp<T, EPI, MATH>(p, s);
       return hipErrorInvalidValue;
     }
     if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
@@ -1228,18 +1472,21 @@ __global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int la
   __syncthreads();
   for (int j = ty; j < 32; j += 8) {
     const int n = bx + j, k = by + tx;  // output row n (input column), column k
-    if (n < cols && k < rows) out[(size_t)packed_row(n, cols, layout) * rows + k] = tile[tx][j];
+    if (n < cols && k < rows) out[packed_offset(n, k, cols, rows, layout)] = tile[tx][j];
   }
 }
 
-// out[packed_row(n), :] = in[n, :], one row per block of 64 threads x 16 B.
-__global__ void pack_rows_kernel(const char* in, size_t ld_bytes, int N, size_t row_bytes,
+// Packed row n of an [N, K] matrix, one row per block of 64 threads x 16 B
+// (8 elements of 16-bit types, 4 of fp32: a 16-byte chunk never straddles
+// a tiled 16-byte slot).
+__global__ void pack_rows_kernel(const char* in, size_t ld_bytes, int N, int K, int esz,
                                  char* out, int layout) {
   const int n = blockIdx.x;
   const char* src = in + (size_t)n * ld_bytes;
-  char* dst = out + (size_t)packed_row(n, N, layout) * row_bytes;
-  for (size_t b = (size_t)threadIdx.x * 16; b < row_bytes; b += 64 * 16)
-    *(u32x4_t*)(dst + b) = *(const u32x4_t*)(src + b);
+  const int epc = 16 / esz;
+  for (int k = threadIdx.x * epc; k < K; k += 64 * epc)
+    *(u32x4_t*)(out + packed_offset(n, k, N, K, layout) * esz) =
+        *(const u32x4_t*)(src + (size_t)k * esz);
 }
 
 __global__ void pack_vec_kernel(const float* in, int N, float* out, int layout) {
@@ -1251,8 +1498,8 @@ hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, voi
                             int layout, hipStream_t s) {
   const size_t esz = dtype == F32 ? 4 : 2;
   if (((uintptr_t)in | (uintptr_t)out | (ld * esz) | (K * esz)) & 15) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(pack_rows_kernel, dim3(N), dim3(64), 0, s, (const char*)in, ld * esz, N,
-                     K * esz, (char*)out, layout);
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(N), dim3(64), 0, s, (const char*)in, ld * esz, N, K,
+                     (int)esz, (char*)out, layout);
   return hipGetLastError();
 }
 

@@ -56,6 +56,20 @@ __host__ __device__ inline int packed_row(int n, int N, int layout) {
   }
 }
 
+// Element offset of (packed row r, column k) in a packed [N, K] weight
+// matrix.  The ping-pong layouts (16-bit, N % 256 == 0, K % 32 == 0) are
+// stored tiled: block (r / 256, k / 32) is 256 rows x 32 columns, 16 KB,
+// blocks ordered by row tile then K slice; inside a block, row r % 256 is 64
+// bytes whose 16-byte chunk c sits in slot c ^ ((r % 256) >> 1 & 3).  That is
+// the GEMMs' LDS image of a weight K slice, so each is one contiguous DMA.
+// The other layouts are row-major.
+__host__ __device__ inline size_t packed_offset(int n, int k, int N, int K, int layout) {
+  const int r = packed_row(n, N, layout);
+  if (layout < PACK_LANE16) return (size_t)r * K + k;
+  const int rr = r % 256, slot = ((k % 32) / 8) ^ ((rr >> 1) & 3);
+  return ((size_t)(r / 256) * (K / 32) + k / 32) * 8192 + rr * 32 + slot * 8 + k % 8;
+}
+
 struct GemmEpilogue {
   int kind = EPI_STORE;
   int math = 0;                    // MathMode for GELU / tanh / silu
@@ -94,11 +108,12 @@ hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N
                                void* C, int ldc, const float* bias, int act, int math,
                                hipStream_t stream);
 
-// out[packed_row(n), k] = in[k, n] (dtype elements): [rows = K, cols = N] to
-// a packed [N, K] weight matrix.
+// Packed (n, k) = in[k, n] (dtype elements, packed_offset): [rows = K,
+// cols = N] to a packed [N, K] weight matrix.
 hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
                             int layout, hipStream_t stream);
-// out[packed_row(n), :] = in[n, :] for an [N, K] matrix with row stride ld.
+// Packed (n, :) = in[n, :] (packed_offset) for an [N, K] matrix with row
+// stride ld.
 hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, void* out,
                             int layout, hipStream_t stream);
 // out[packed_row(n)] = in[n] for an fp32 vector of N.
