@@ -513,36 +513,38 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_lds_kernel(GemmParams p) {
 // lane stores 16 bytes at a time.  The bias is read in packed order.
 // ---------------------------------------------------------------------------
 template <typename T>
-__device__ inline void store8(T* dst, float4_t a, float4_t b) {
+__device__ inline u32x4_t pack8(float4_t a, float4_t b) {
   if constexpr (Elem<T>::dtype == F16) {
     half8_t h = {(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
                  (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
-    *(half8_t*)dst = h;
+    return __builtin_bit_cast(u32x4_t, h);
   } else {
     bf16x8_t h = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
                   (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
-    *(bf16x8_t*)dst = h;
+    return __builtin_bit_cast(u32x4_t, h);
   }
 }
 
+template <typename T>
+__device__ inline void store8(T* dst, float4_t a, float4_t b) {
+  *(u32x4_t*)dst = pack8<T>(a, b);
+}
+
 // One 16-row block of a 64-feature group: v[f] is accumulator tile f of the
-// group for token rows m - (lane & 15) .. +15 (lane holds row m); nbase is
-// the group's first (packed) output column.
-template <typename T, int EPI, int MATH, bool BIAS>
-__device__ __attribute__((always_inline)) inline void pp_epilogue_block(const GemmParams& p,
-                                                                        float4_t (&v)[4], int m,
-                                                                        int nbase, int lane) {
-  T* C = (T*)p.C;
+// group for the lane's token row; nbase is the group's first (packed) output
+// column.  bias_at(f) gives the bias of tile f (added when BIAS), rope_at(k)
+// the (cos, sin) float4 k of the row's position in the group's RoPE table
+// (asked for every group; ignored past rope_cols).  The results go out
+// through put(col, a, b): eight outputs of the lane's row starting at output
+// column col.
+template <typename T, int EPI, int MATH, bool BIAS, typename BiasAt, typename RopeAt, typename Put>
+__device__ __attribute__((always_inline)) inline void pp_epilogue_block(
+    const GemmParams& p, float4_t (&v)[4], int nbase, int lane, BiasAt&& bias_at,
+    RopeAt&& rope_at, Put&& put) {
   const int g = lane >> 4;
-  // Rows past M are computed on row M-1's inputs and not stored.
-  const bool ok = m < p.M;
-  const int mc = ok ? m : p.M - 1;
-  T* crow = C + (size_t)mc * p.ldc;
   if constexpr (BIAS) {
-    if (p.epi.bias) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f) v[f] += *(const float4_t*)(p.epi.bias + nbase + f * 16 + g * 4);
-    }
+    for (int f = 0; f < 4; ++f) v[f] += bias_at(f);
   }
   if constexpr (EPI == EPI_SWIGLU) {
     // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
@@ -552,34 +554,32 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue_block(const Ge
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(v[2 * h][i]) * v[2 * h + 1][i];
     }
-    if (ok) store8<T>(crow + nbase / 2 + g * 8, o[0], o[1]);
+    put(nbase / 2 + g * 8, o[0], o[1]);
   } else if constexpr (EPI == EPI_ROPE) {
     // PACK_ROPE: tiles 0 / 1 hold dims 8g+i / 8g+4+i of the head, tiles
-    // 2 / 3 their rotate-half partners 32+8g+i / 32+8g+4+i.
-    if (nbase < p.epi.rope_cols) {
+    // 2 / 3 their rotate-half partners 32+8g+i / 32+8g+4+i.  Heads past
+    // rope_cols rotate by the identity (cos 1, sin 0), which leaves them
+    // unchanged; the code stays free of branches.
+    const bool rot = nbase < p.epi.rope_cols;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
 #pragma clang fp contract(off)
-      const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
-      const float4_t* cs = (const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8);
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
+      for (int h = 0; h < 2; ++h) {
+        float4_t c = rope_at(f * 2 + h);  // (cos, sin) of dims 8g + 4f + 2h, +1
+        c = rot ? c : float4_t{1.f, 0.f, 1.f, 0.f};
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float4_t c = cs[f * 2 + h];  // (cos, sin) of dims 8g + 4f + 2h, +1
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int i = 2 * h + e;
-            const float x1 = v[f][i], x2 = v[f + 2][i];
-            const float co = c[2 * e], si = c[2 * e + 1];
-            v[f][i] = x1 * co - x2 * si;
-            v[f + 2][i] = x1 * si + x2 * co;
-          }
+        for (int e = 0; e < 2; ++e) {
+          const int i = 2 * h + e;
+          const float x1 = v[f][i], x2 = v[f + 2][i];
+          const float co = c[2 * e], si = c[2 * e + 1];
+          v[f][i] = x1 * co - x2 * si;
+          v[f + 2][i] = x1 * si + x2 * co;
         }
       }
     }
-    if (ok) {
-      store8<T>(crow + nbase + g * 8, v[0], v[1]);
-      store8<T>(crow + nbase + 32 + g * 8, v[2], v[3]);
-    }
+    put(nbase + g * 8, v[0], v[1]);
+    put(nbase + 32 + g * 8, v[2], v[3]);
   } else {
     // PACK_LANE16: tile f holds outputs 16g+4f+i.
 #pragma unroll
@@ -588,10 +588,8 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue_block(const Ge
 #pragma unroll
       for (int f = 0; f < 4; ++f) v[f] *= p.epi.q_scale;
     }
-    if (ok) {
-      store8<T>(crow + nbase + g * 16, v[0], v[1]);
-      store8<T>(crow + nbase + g * 16 + 8, v[2], v[3]);
-    }
+    put(nbase + g * 16, v[0], v[1]);
+    put(nbase + g * 16 + 8, v[2], v[3]);
   }
 }
 
@@ -607,7 +605,23 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmPara
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     float4_t v[4] = {acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
-    pp_epilogue_block<T, EPI, MATH, BIAS>(p, v, m0 + wm_off + t * 16 + (lane & 15), nbase, lane);
+    // Rows past M are computed on row M-1's inputs and not stored.
+    const int m = m0 + wm_off + t * 16 + (lane & 15);
+    const int mc = m < p.M ? m : p.M - 1;
+    T* crow = (T*)p.C + (size_t)m * p.ldc;
+    const int g = lane >> 4;
+    auto bias_at = [&](int f) { return *(const float4_t*)(p.epi.bias + nbase + f * 16 + g * 4); };
+    auto rope_at = [&](int k) {
+      const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
+      return ((const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8))[k];
+    };
+    auto put = [&](int col, float4_t a, float4_t b) {
+      if (m < p.M) store8<T>(crow + col, a, b);
+    };
+    if (BIAS && p.epi.bias)
+      pp_epilogue_block<T, EPI, MATH, BIAS>(p, v, nbase, lane, bias_at, rope_at, put);
+    else
+      pp_epilogue_block<T, EPI, MATH, false>(p, v, nbase, lane, bias_at, rope_at, put);
     // One row block at a time: hoisting every block's table loads would
     // need more registers than the accumulators leave.
     __builtin_amdgcn_sched_barrier(0);
@@ -1013,6 +1027,15 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
 // step s each wave waits until its own loads of step s+2 have landed; after
 // the barrier every wave's have.
 // ---------------------------------------------------------------------------
+// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled.
+template <int N, int I = 0, typename F>
+__device__ __attribute__((always_inline)) inline void w4_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    w4_for<N, I + 1>(f);
+  }
+}
+
 // The K-step blocks set m0 (the LDS address of DMA loads) themselves; the
 // compiler emits no m0 use of its own in this kernel.
 #pragma clang diagnostic push
@@ -1037,7 +1060,8 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
   constexpr bool F16T = Elem<T>::dtype == F16;
   static_assert(NS == 4, "the K loop runs in groups of four steps, one per stage");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  // NS stages, then a 4 KB epilogue staging area per wave.
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 4 * 4096];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
   const int lane = threadIdx.x & 63;
@@ -1149,35 +1173,104 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 
   // Epilogue: accumulator tiles come out four at a time (one 16-row block
   // of one 64-feature group), so the compiler's registers stay below v128.
-  auto epilogue = [&](int ti) __attribute__((always_inline)) {
+  // Each 16-row block of the wave's outputs (RB bytes per row) is assembled
+  // row-major in the wave's LDS staging area (16-byte chunk c of row r in
+  // slot c ^ (r % CPRW)) and stored from there as whole rows: every store
+  // instruction writes 64/CPRW rows of RB contiguous bytes, where the
+  // accumulator layout alone would scatter 16-byte pieces over 16 rows.
+  // RoPE tiles go out one 64-feature group at a time (128-byte rows), so
+  // that only one group's tables are held (and prefetched) at once.
+  constexpr bool PER_GROUP = EPI == EPI_ROPE;
+  constexpr int RB = PER_GROUP || EPI == EPI_SWIGLU ? 128 : 256, CPRW = RB / 16;
+  constexpr int NUNITS = PER_GROUP ? 16 : 8;
+  // Every load of the epilogue (bias, positions, RoPE tables) is issued
+  // before the stores that precede its use: the memory counter completes in
+  // issue order, so a wait for a load issued after a store would also wait
+  // for the store.  RoPE tables are fetched one unit ahead.
+  // (The bias test is hoisted out of the epilogue so that its code has no
+  // data-dependent branches around loads: the compiler's wait counts stay
+  // exact only on straight-line code.)
+  auto epilogue_hb = [&](int ti, auto hbc) __attribute__((always_inline)) {
+    constexpr bool HB = decltype(hbc)::value;
     int m0, n0;
     coords(ti, m0, n0);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     // The last MFMAs' results must be written before they are read.
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-    const int mrow = m0 + wm * 128 + (ln & 15);
-    auto block = [&](auto tc, auto hc) __attribute__((always_inline)) {
-      constexpr int t = decltype(tc)::value, h = decltype(hc)::value;
-      float4_t v[4] = {W4Acc<(4 * h + 0) * 8 + t>::read(), W4Acc<(4 * h + 1) * 8 + t>::read(),
-                       W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
-      pp_epilogue_block<T, EPI, MATH, EPI != EPI_ROPE>(p, v, mrow + t * 16,
-                                                       n0 + wn * 128 + h * 64, ln);
+    const int r = ln & 15, g = ln >> 4;
+    const int mrow = m0 + wm * 128 + r;
+    const int cbase = n0 + wn * 128;  // the wave's first packed feature
+    char* stg = lds + NS * STAGE + wave * 4096;
+    float4_t bv[2][4];
+    if constexpr (HB) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+          bv[h][f] = *(const float4_t*)(p.epi.bias + cbase + h * 64 + f * 16 + g * 4);
+    }
+    int pos[8];
+    float4_t cs[2][4];  // [unit parity][k]
+    if constexpr (EPI == EPI_ROPE) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) pos[t] = p.epi.pos[min(mrow + t * 16, p.M - 1)];
+    }
+    // Unit u: row block t = u % 8 of group h = u / 8 (PER_GROUP), or row
+    // block u of both groups.
+    auto fetch_cs = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      if constexpr (EPI == EPI_ROPE && u < NUNITS) {
+        // Loaded for every group (in bounds; unused past rope_cols).
+        constexpr int t = u % 8, h = u / 8;
+        const float2* table = cbase + h * 64 < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
+        const float4_t* src = (const float4_t*)(table + (size_t)pos[t] * 32 + g * 8);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) cs[u & 1][k] = src[k];
+      }
+    };
+    auto unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      constexpr int t = PER_GROUP ? u % 8 : u;
+      const int col0 = PER_GROUP ? cbase + (u / 8) * 64 : (EPI == EPI_SWIGLU ? cbase / 2 : cbase);
+      fetch_cs(std::integral_constant<int, u + 1>{});
+      auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
+        const int c = (col - col0) >> 3;
+        *(u32x4_t*)(stg + r * RB + ((c ^ (r % CPRW)) << 4)) = pack8<T>(a, b);
+      };
+      auto block = [&](auto hc) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
+        float4_t v[4] = {W4Acc<(4 * h + 0) * 8 + t>::read(), W4Acc<(4 * h + 1) * 8 + t>::read(),
+                         W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
+        pp_epilogue_block<T, EPI, MATH, HB>(
+            p, v, cbase + h * 64, ln, [&](int f) { return bv[h][f]; },
+            [&](int k) { return cs[u & 1][k]; }, put);
+      };
+      if constexpr (PER_GROUP) {
+        block(std::integral_constant<int, u / 8>{});
+      } else {
+        block(I0{});
+        block(I1{});
+      }
+      const int c = ln % CPRW;
+#pragma unroll
+      for (int k = 0; k < CPRW / 4; ++k) {
+        const int rr = ln / CPRW + k * (64 / CPRW);
+        const u32x4_t val = *(const u32x4_t*)(stg + rr * RB + ((c ^ (rr % CPRW)) << 4));
+        // Rows past M hold row M-1's outputs (computed from its inputs) and
+        // are stored there again: the same bytes, and no branch.
+        const int m = min(m0 + wm * 128 + t * 16 + rr, p.M - 1);
+        *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + col0 + c * 8) = val;
+      }
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto row = [&](auto tc) __attribute__((always_inline)) {
-      block(tc, I0{});
-      block(tc, I1{});
-    };
-    row(I0{});
-    row(I1{});
-    row(I2{});
-    row(I3{});
-    row(std::integral_constant<int, 4>{});
-    row(std::integral_constant<int, 5>{});
-    row(std::integral_constant<int, 6>{});
-    row(std::integral_constant<int, 7>{});
+    fetch_cs(I0{});
+    w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
     asm volatile("" ::: "memory");
+  };
+  auto epilogue = [&](int ti) __attribute__((always_inline)) {
+    if (EPI != EPI_ROPE && p.epi.bias) epilogue_hb(ti, std::true_type{});
+    else epilogue_hb(ti, std::false_type{});
   };
 
   // Per tile: group 0 (its first step multiplies into zero), groups 1 ..
