@@ -1060,8 +1060,8 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
   constexpr bool F16T = Elem<T>::dtype == F16;
   static_assert(NS == 4, "the K loop runs in groups of four steps, one per stage");
-  // NS stages, then a 4 KB epilogue staging area per wave.
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 4 * 4096];
+  // NS stages, then an 8 KB epilogue staging area per wave.
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 4 * 8192];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
   const int lane = threadIdx.x & 63;
@@ -1120,36 +1120,40 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   const uint32_t rdB = lds0 + (uint32_t)(BM * ROWB + (wn * 128 + fr) * ROWB) + co;
   const uint32_t dma0 = lds0 + (uint32_t)wave * 4096;
 
-  // Prologue: steps 0 .. 2 into stages 0 .. 2; fragments of step 0 into
-  // register set 0.
-  load_tile(0);
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s) {
+  // DMA of the cursor's step into stage st, then advance the cursor.
+  auto load_step = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NLD; ++j)
-      w4_dma(dma0 + s * STAGE + (j < 4 ? j * 1024 : BM * ROWB + (j - 4) * 1024), off[j],
+      w4_dma(dma0 + st * STAGE + (j < 4 ? j * 1024 : BM * ROWB + (j - 4) * 1024), off[j],
              j < 4 ? ka : kb);
     ka += BK * sizeof(T);
     kb += KB_STEP;
-  }
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NLD * (NS - 3)) : "memory");
+  };
+
+  // Prologue: steps 0 .. 3 into stages 0 .. 3; wait for steps 0 and 1;
+  // fragments of step 0 into register set 0.
+  load_tile(0);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) load_step(s);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NLD) : "memory");
   asm volatile(FL_W4_READ_0 ::"v"(rdA), "v"(rdB) : "memory", FL_W4_CLOBBER_V);
 
   // K step j of a group of four (global step s = j mod 4, since every tile
   // has a multiple of four steps): register set j % 2, reads stage (j+1)%4,
   // loads the cursor's step into stage (j+3)%4, then advances the cursor.
-  // It first waits for its own loads of step s+1 (all but the last 8 loads
-  // issued), except in a tile's first step (Z): the wait before the
-  // epilogue already covered step s+1, and waiting here would also wait for
-  // the epilogue's stores.
-  auto kstep = [&](auto jc, auto zero) __attribute__((always_inline)) {
+  // It first waits (vmcnt VM) until its own loads of step s+1 have landed.
+  // A tile's first step (Z) loads nothing: its slice, step 3, went out
+  // before the previous tile's epilogue, so that the next two steps' waits
+  // can let the epilogue's stores stay outstanding.
+  auto kstep = [&](auto jc, auto zero, auto vmc) __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
     constexpr bool Z = decltype(zero)::value;
+    constexpr int VM = decltype(vmc)::value;
     constexpr uint32_t RD = ((J + 1) % NS) * STAGE, DM = ((J + NS - 1) % NS) * STAGE;
 #define FL_W4_ARGS                                                                          \
   ::"v"(rdA + RD), "v"(rdB + RD), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),        \
       "v"(off[4]), "v"(off[5]), "v"(off[6]), "v"(off[7]), "s"(dma0 + DM), "s"(ka), "s"(kb),  \
-      "n"(Z ? 63 : NLD * (NS - 3))                                                         \
+      "n"(VM)                                                                              \
   : "memory", "m0", "scc", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A
     if constexpr (F16T) {
       if constexpr (J % 2 == 0 && !Z) asm volatile(FL_W4_STEP_F16_0_0 FL_W4_ARGS);
@@ -1163,8 +1167,10 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       if constexpr (J % 2 == 1 && Z) asm volatile(FL_W4_STEP_BF16_1_1 FL_W4_ARGS);
     }
 #undef FL_W4_ARGS
-    ka += BK * sizeof(T);
-    kb += KB_STEP;
+    if constexpr (!Z) {
+      ka += BK * sizeof(T);
+      kb += KB_STEP;
+    }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1178,15 +1184,15 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // slot c ^ (r % CPRW)) and stored from there as whole rows: every store
   // instruction writes 64/CPRW rows of RB contiguous bytes, where the
   // accumulator layout alone would scatter 16-byte pieces over 16 rows.
-  // RoPE tiles go out one 64-feature group at a time (128-byte rows), so
-  // that only one group's tables are held (and prefetched) at once.
-  constexpr bool PER_GROUP = EPI == EPI_ROPE;
-  constexpr int RB = PER_GROUP || EPI == EPI_SWIGLU ? 128 : 256, CPRW = RB / 16;
-  constexpr int NUNITS = PER_GROUP ? 16 : 8;
-  // Every load of the epilogue (bias, positions, RoPE tables) is issued
-  // before the stores that precede its use: the memory counter completes in
-  // issue order, so a wait for a load issued after a store would also wait
-  // for the store.  RoPE tables are fetched one unit ahead.
+  // A unit is one 16-row block of the wave's outputs (both feature groups).
+  constexpr int RB = EPI == EPI_SWIGLU ? 128 : 256, CPRW = RB / 16;
+  constexpr int NUNITS = 8, RD = 2;
+  // Loads of the epilogue (bias, positions) are issued before its first
+  // store: the memory counter completes in issue order, so a wait for a
+  // load issued after a store would also wait for the store.  RoPE tables
+  // (the same table and rows for both heads of the wave: gemm_w4_ok) are
+  // fetched RD units ahead, so that the stores a table load queues behind
+  // have had RD units of time to complete.
   // (The bias test is hoisted out of the epilogue so that its code has no
   // data-dependent branches around loads: the compiler's wait counts stay
   // exact only on straight-line code.)
@@ -1201,7 +1207,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     const int r = ln & 15, g = ln >> 4;
     const int mrow = m0 + wm * 128 + r;
     const int cbase = n0 + wn * 128;  // the wave's first packed feature
-    char* stg = lds + NS * STAGE + wave * 4096;
+    char* stg = lds + NS * STAGE + wave * 8192;
     float4_t bv[2][4];
     if constexpr (HB) {
 #pragma unroll
@@ -1211,32 +1217,32 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
           bv[h][f] = *(const float4_t*)(p.epi.bias + cbase + h * 64 + f * 16 + g * 4);
     }
     int pos[8];
-    float4_t cs[2][4];  // [unit parity][k]
+    float4_t cs[RD + 1][4];  // [unit % (RD + 1)][k]
     if constexpr (EPI == EPI_ROPE) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) pos[t] = p.epi.pos[min(mrow + t * 16, p.M - 1)];
     }
-    // Unit u: row block t = u % 8 of group h = u / 8 (PER_GROUP), or row
-    // block u of both groups.
+    const float2* table = cbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
     auto fetch_cs = [&](auto uc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       if constexpr (EPI == EPI_ROPE && u < NUNITS) {
-        // Loaded for every group (in bounds; unused past rope_cols).
-        constexpr int t = u % 8, h = u / 8;
-        const float2* table = cbase + h * 64 < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
-        const float4_t* src = (const float4_t*)(table + (size_t)pos[t] * 32 + g * 8);
+        // Loaded for every tile (in bounds; unused past rope_cols).
+        const float4_t* src = (const float4_t*)(table + (size_t)pos[u] * 32 + g * 8);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) cs[u & 1][k] = src[k];
+        for (int k = 0; k < 4; ++k) cs[u % (RD + 1)][k] = src[k];
       }
     };
-    auto unit = [&](auto uc) __attribute__((always_inline)) {
+    // Unit u is assembled in staging buffer u % 2 and stored while unit u+1
+    // is computed, so the LDS round trip of one overlaps the other's math.
+    const int col0 = EPI == EPI_SWIGLU ? cbase / 2 : cbase;
+    auto compute_unit = [&](auto uc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
-      constexpr int t = PER_GROUP ? u % 8 : u;
-      const int col0 = PER_GROUP ? cbase + (u / 8) * 64 : (EPI == EPI_SWIGLU ? cbase / 2 : cbase);
-      fetch_cs(std::integral_constant<int, u + 1>{});
+      constexpr int t = u;
+      char* buf = stg + (u & 1) * 4096;
+      fetch_cs(std::integral_constant<int, u + RD>{});
       auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
         const int c = (col - col0) >> 3;
-        *(u32x4_t*)(stg + r * RB + ((c ^ (r % CPRW)) << 4)) = pack8<T>(a, b);
+        *(u32x4_t*)(buf + r * RB + ((c ^ (r % CPRW)) << 4)) = pack8<T>(a, b);
       };
       auto block = [&](auto hc) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
@@ -1244,28 +1250,35 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
                          W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
         pp_epilogue_block<T, EPI, MATH, HB>(
             p, v, cbase + h * 64, ln, [&](int f) { return bv[h][f]; },
-            [&](int k) { return cs[u & 1][k]; }, put);
+            [&](int k) { return cs[u % (RD + 1)][k]; }, put);
       };
-      if constexpr (PER_GROUP) {
-        block(std::integral_constant<int, u / 8>{});
-      } else {
-        block(I0{});
-        block(I1{});
-      }
+      block(I0{});
+      block(I1{});
+    };
+    auto store_unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      constexpr int t = u;
+      const char* buf = stg + (u & 1) * 4096;
       const int c = ln % CPRW;
 #pragma unroll
       for (int k = 0; k < CPRW / 4; ++k) {
         const int rr = ln / CPRW + k * (64 / CPRW);
-        const u32x4_t val = *(const u32x4_t*)(stg + rr * RB + ((c ^ (rr % CPRW)) << 4));
+        const u32x4_t val = *(const u32x4_t*)(buf + rr * RB + ((c ^ (rr % CPRW)) << 4));
         // Rows past M hold row M-1's outputs (computed from its inputs) and
         // are stored there again: the same bytes, and no branch.
         const int m = min(m0 + wm * 128 + t * 16 + rr, p.M - 1);
         *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + col0 + c * 8) = val;
       }
+    };
+    auto unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      compute_unit(uc);
+      if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{});
       __builtin_amdgcn_sched_barrier(0);
     };
-    fetch_cs(I0{});
+    w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
     w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
+    store_unit(std::integral_constant<int, NUNITS - 1>{});
     asm volatile("" ::: "memory");
   };
   auto epilogue = [&](int ti) __attribute__((always_inline)) {
@@ -1275,26 +1288,48 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 
   // Per tile: group 0 (its first step multiplies into zero), groups 1 ..
   // G-2, and the last group, whose steps 1-3 load the next tile's steps 0-2
-  // (past the last tile: its step 0 again, in bounds and never read).
+  // (past the last tile: its steps again, in bounds and never read).  Then
+  // step 3 of the next tile goes into stage 3 (free since step 2 of this
+  // group) ahead of the epilogue.
+  //
+  // Wait counts: every wave's memory operations complete in issue order.
+  // The epilogue issues exactly EST stores (no loads once its stores start
+  // but RoPE's, which only add to the count), so in the next tile step 1
+  // (needing step 2) and step 2 (needing step 3) find at least EST + 8
+  // operations issued after the loads they need.  Everything else waits
+  // with 8 outstanding: the one step loaded since.
+  constexpr int EST = EPI == EPI_SWIGLU ? 16 : 32;
+  using VM8 = std::integral_constant<int, NLD>;
+  using VME = std::integral_constant<int, NLD + EST>;
+  using VM63 = std::integral_constant<int, 63>;
+  using Z1 = std::true_type;
+  using Z0 = std::false_type;
   const int G4 = nk / 4;
   for (int ti = 0; ti < my_tiles; ++ti) {
-    kstep(I0{}, std::true_type{});
-    kstep(I1{}, std::false_type{});
-    kstep(I2{}, std::false_type{});
-    kstep(I3{}, std::false_type{});
-    for (int g = 1; g < G4 - 1; ++g) {
-      kstep(I0{}, std::false_type{});
-      kstep(I1{}, std::false_type{});
-      kstep(I2{}, std::false_type{});
-      kstep(I3{}, std::false_type{});
+    kstep(I0{}, Z1{}, VM63{});
+    if (ti == 0) {
+      kstep(I1{}, Z0{}, VM8{});
+      kstep(I2{}, Z0{}, VM8{});
+    } else {
+      kstep(I1{}, Z0{}, VME{});
+      kstep(I2{}, Z0{}, VME{});
     }
-    kstep(I0{}, std::false_type{});
+    kstep(I3{}, Z0{}, VM8{});
+    for (int g = 1; g < G4 - 1; ++g) {
+      kstep(I0{}, Z0{}, VM8{});
+      kstep(I1{}, Z0{}, VM8{});
+      kstep(I2{}, Z0{}, VM8{});
+      kstep(I3{}, Z0{}, VM8{});
+    }
+    kstep(I0{}, Z0{}, VM8{});
     load_tile(ti + 1 < my_tiles ? ti + 1 : ti);
-    kstep(I1{}, std::false_type{});
-    kstep(I2{}, std::false_type{});
-    kstep(I3{}, std::false_type{});
-    // Step 1 of the next tile (loaded in step 2 of this group) has landed.
+    kstep(I1{}, Z0{}, VM8{});
+    kstep(I2{}, Z0{}, VM8{});
+    kstep(I3{}, Z0{}, VM8{});
+    // Steps 0 and 1 of the next tile have landed (step 1 is read in its
+    // first step); step 3 goes out before the stores.
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
+    load_step(3);
     epilogue(ti);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1364,6 +1399,15 @@ static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The four-wave kernel's K loop runs in groups of four steps with at least
+// two groups per tile; its RoPE epilogue gives both 64-feature heads of a
+// wave the same table and rotation.
+static bool gemm_w4_ok(const GemmParams& p) {
+  if (!FL_GEMM_W4 || p.K % 128 || p.K < 256) return false;
+  if (p.epi.kind == EPI_ROPE && (p.epi.q_cols % 128 || p.epi.rope_cols % 128)) return false;
+  return true;
+}
+
 template <typename T, int EPI, int MATH>
 static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
@@ -1392,8 +1436,7 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     // epilogues it was built for reach this point with such a layout.
     if (p.epi.layout >= PACK_LANE16) {
       if constexpr (pp_epilogue_ok(EPI, MATH))
-        return FL_GEMM_W4 && p.K % 128 == 0 && p.K >= 256 ? launch_w4<T, EPI, MATH>(p, s)
-                                                         : launch_pp<T, EPI, MATH>(p, s);
+        return gemm_w4_ok(p) ? launch_w4<T, EPI, MATH>(p, s) : launch_pp<T, EPI, MATH>(p, s);
       return hipErrorInvalidValue;
     }
     if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
