@@ -1097,17 +1097,21 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   const char* ka = nullptr;  // DMA cursor: token / weight base of the next K slice to load
   const char* kb = nullptr;
   constexpr size_t KB_STEP = (size_t)BN * BK * sizeof(T);  // one tiled weight block
+  const bool a_tiled = p.epi.a_tiled;
+  const size_t KA_STEP = a_tiled ? (size_t)BM * BK * sizeof(T) : BK * sizeof(T);
   auto load_tile = [&](int ti) __attribute__((always_inline)) {
     int m0, n0;
     coords(ti, m0, n0);
-    ka = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
+    ka = a_tiled ? (const char*)p.A + (size_t)(m0 / BM) * nk * KA_STEP
+                 : (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
     kb = (const char*)p.B + (size_t)(n0 / BN) * nk * KB_STEP;
     const int lim = p.M - 1 - m0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = wave * 64 + j * 16 + lrow;
       const int c = lcol ^ pp_swz<4>(row);
-      off[j] = (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
+      off[j] = a_tiled ? (uint32_t)((wave * 4 + j) * 1024 + lane * 16)
+                       : (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
       off[4 + j] = (uint32_t)((wave * 4 + j) * 1024 + lane * 16);
     }
   };
@@ -1126,7 +1130,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     for (int j = 0; j < NLD; ++j)
       w4_dma(dma0 + st * STAGE + (j < 4 ? j * 1024 : BM * ROWB + (j - 4) * 1024), off[j],
              j < 4 ? ka : kb);
-    ka += BK * sizeof(T);
+    ka += KA_STEP;
     kb += KB_STEP;
   };
 
@@ -1168,7 +1172,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     }
 #undef FL_W4_ARGS
     if constexpr (!Z) {
-      ka += BK * sizeof(T);
+      ka += KA_STEP;
       kb += KB_STEP;
     }
   };
@@ -1259,6 +1263,23 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
       const char* buf = stg + (u & 1) * 4096;
+      if constexpr (EPI == EPI_SWIGLU) {
+        if (p.epi.out_tiled) {
+          // Tiled output: the unit's 16 rows of each 32-column K slice are one
+          // contiguous 1 KB block; lane l writes row l/4, slot l%4 of it.  Rows
+          // past M hold row M-1's outputs: they fill the tile's last rows.
+          const int rr = ln >> 2, slot = ln & 3;
+          const int trow = wm * 128 + t * 16;  // first row of the unit in its 256-row tile
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const int cc = kk * 4 + (slot ^ ((rr >> 1) & 3));
+            const u32x4_t val = *(const u32x4_t*)(buf + rr * RB + ((cc ^ (rr % CPRW)) << 4));
+            const size_t blk = (size_t)(m0 / 256) * (p.ldc / 32) + col0 / 32 + kk;
+            *(u32x4_t*)((T*)p.C + blk * 8192 + trow * 32 + ln * 8) = val;
+          }
+          return;
+        }
+      }
       const int c = ln % CPRW;
 #pragma unroll
       for (int k = 0; k < CPRW / 4; ++k) {
@@ -1402,8 +1423,9 @@ static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
 // The four-wave kernel's K loop runs in groups of four steps with at least
 // two groups per tile; its RoPE epilogue gives both 64-feature heads of a
 // wave the same table and rotation.
+static bool gemm_w4_shape_ok(int K) { return FL_GEMM_W4 && K % 128 == 0 && K >= 256; }
 static bool gemm_w4_ok(const GemmParams& p) {
-  if (!FL_GEMM_W4 || p.K % 128 || p.K < 256) return false;
+  if (!gemm_w4_shape_ok(p.K)) return false;
   if (p.epi.kind == EPI_ROPE && (p.epi.q_cols % 128 || p.epi.rope_cols % 128)) return false;
   return true;
 }
@@ -1435,8 +1457,11 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     // B packed for the ping-pong kernel (gemm_pp_layout) goes there; only the
     // epilogues it was built for reach this point with such a layout.
     if (p.epi.layout >= PACK_LANE16) {
-      if constexpr (pp_epilogue_ok(EPI, MATH))
-        return gemm_w4_ok(p) ? launch_w4<T, EPI, MATH>(p, s) : launch_pp<T, EPI, MATH>(p, s);
+      if constexpr (pp_epilogue_ok(EPI, MATH)) {
+        if (gemm_w4_ok(p)) return launch_w4<T, EPI, MATH>(p, s);
+        if (p.epi.out_tiled || p.epi.a_tiled) return hipErrorInvalidValue;
+        return launch_pp<T, EPI, MATH>(p, s);
+      }
       return hipErrorInvalidValue;
     }
     if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
@@ -1479,9 +1504,22 @@ int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bia
   return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
 }
 
+bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
+                   bool a_tiled) {
+  if (!out_tiled && !a_tiled) return true;
+  if (gemm_pp_layout(dtype, N, K, epi_kind, math, has_bias) < 0 || !gemm_w4_shape_ok(K))
+    return false;
+  if (out_tiled && (epi_kind != EPI_SWIGLU || (N / 2) % 32)) return false;
+  if (a_tiled && epi_kind != EPI_STORE) return false;
+  return true;
+}
+
 bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, const void* B,
                        int ldb, const void* C, int ldc, const GemmEpilogue& epi) {
   if (M <= 0 || N <= 0 || K <= 0) return false;
+  if (!gemm_tiled_ok(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr, epi.out_tiled,
+                     epi.a_tiled))
+    return false;
   if (epi.layout >= PACK_LANE16) {
     if (gemm_pp_layout(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr) != epi.layout)
       return false;

@@ -86,7 +86,27 @@ struct GemmEpilogue {
   int q_cols = 0;
   float q_scale = 1.0f;
   const float2* rope_cs_q = nullptr;
+  // Tiled activations (four-wave kernel only, gemm_tiled_ok): out_tiled
+  // writes the SwiGLU output C in the weights' tiled layout (tiled_act_offset)
+  // with rows up to a multiple of 256; a_tiled reads A that way.  Rows past M
+  // of the last tile hold copies of row M-1, so they can be read as operand
+  // rows like any other.
+  bool out_tiled = false;
+  bool a_tiled = false;
 };
+
+// Element offset of (row m, column k) of an activation matrix with K columns
+// stored tiled: the layout of packed_offset for a ping-pong weight matrix.
+__host__ __device__ inline size_t tiled_act_offset(int64_t m, int k, int K) {
+  const int rr = (int)(m % 256), slot = ((k % 32) / 8) ^ ((rr >> 1) & 3);
+  return ((size_t)(m / 256) * (K / 32) + k / 32) * 8192 + rr * 32 + slot * 8 + k % 8;
+}
+
+// Whether the tiled-activation options can be used for this GEMM (the
+// four-wave kernel takes it): 16-bit, ping-pong layout, K % 128 == 0,
+// K >= 256; out_tiled only with the SwiGLU epilogue, a_tiled only with STORE.
+bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
+                   bool a_tiled);
 
 // The packing the ping-pong GEMM needs for this problem, or -1 when that
 // kernel does not take it (the caller then packs PACK_PLAIN / PACK_SWIGLU16

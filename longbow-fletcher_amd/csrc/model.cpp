@@ -23,6 +23,10 @@
 #include "context.hpp"
 #include "kernels.hpp"
 
+#ifndef FL_FFN_TILED
+#define FL_FFN_TILED 1
+#endif
+
 namespace fl {
 
 struct LayerW {
@@ -91,6 +95,9 @@ struct fl_model {
   int n_work = 0, max_len = 0, waves = 4;
   int qblocks = 1;            // query blocks of the longest sequence (flash work items per head)
   bool q_prescaled = false;   // QKV epilogue multiplies Q by scale * log2(e) for the flash kernel
+  // The SwiGLU output (FFN-down's activations) is kept in the tiled layout
+  // (tiled_act_offset), so FFN-down streams it in contiguous 16 KB blocks.
+  bool ffn_tiled = false;
   const float2* rope_cs = nullptr;
   const float2* rope_cs_q = nullptr;  // rope_cs * scale * log2(e), for a pre-scaled Q
 
@@ -398,6 +405,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       if (m->swiglu) {
         if (m->mfma_up) {
           e.kind = EPI_SWIGLU;
+          e.out_tiled = m->ffn_tiled;
           M_ST(gemm(m, true, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
         } else {
           // Unfused: [T, 2I] product, then silu(gate) * up into QKV.
@@ -414,6 +422,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       GemmEpilogue e;
       e.bias = w.bd;
       e.layout = m->lay_down;
+      e.a_tiled = m->ffn_tiled;
       M_ST(gemm(m, m->mfma_down, m->QKV, w.wd, m->TMP, Ti, H, m->I, e));
     }
     {
@@ -495,6 +504,9 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     // ping-pong kernel, whose epilogue applies the scale.
     m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
                      m->H % 64 == 0;
+    m->ffn_tiled = FL_FFN_TILED && m->swiglu && m->lay_up == PACK_SWIGLU_LANE && m->lay_down >= PACK_LANE16 &&
+                   gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, false) &&
+                   gemm_tiled_ok(m->dtype, m->H, m->I, EPI_STORE, c.math, has_bias, false, true);
   }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
