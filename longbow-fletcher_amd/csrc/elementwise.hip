@@ -169,7 +169,7 @@ __global__ void rope_kernel(T* t, int rows, int heads, int hd, int ld, const int
 template <typename T>
 __global__ void __launch_bounds__(256)
 pool_partial_kernel(const T* hidden, int cols, const int* cu, int rows_per_chunk, int max_chunks,
-                    float* part) {
+                    float* part, bool tiled) {
   const int seq = blockIdx.y, chunk = blockIdx.x;
   const int s0 = cu[seq], L = cu[seq + 1] - s0;
   const int r0 = chunk * rows_per_chunk;
@@ -177,7 +177,8 @@ pool_partial_kernel(const T* hidden, int cols, const int* cu, int rows_per_chunk
   const int r1 = min(L, r0 + rows_per_chunk);
   for (int c = threadIdx.x; c < cols; c += blockDim.x) {
     float acc = 0.f;
-    for (int r = r0; r < r1; ++r) acc += to_f(hidden[(size_t)(s0 + r) * cols + c]);
+    for (int r = r0; r < r1; ++r)
+      acc += to_f(hidden[tiled ? tiled_act_offset(s0 + r, c, cols) : (size_t)(s0 + r) * cols + c]);
     dst[c] = acc;
   }
 }
@@ -221,11 +222,23 @@ pool_final_kernel(const float* part, int cols, const int* cu, int rows_per_chunk
 
 template <typename T>
 __global__ void gather_cls_kernel(const T* hidden, int cols, const int* cu, int nseq,
-                                  float* out) {
-  const int64_t total = (int64_t)nseq * cols;
-  FL_GRID_STRIDE(i, total) {
-    const int64_t s = i / cols, c = i % cols;
-    out[i] = to_f(hidden[(size_t)cu[s] * cols + c]);
+                                  float* out, bool tiled) {
+  const int64_t n = (int64_t)nseq * cols;
+  FL_GRID_STRIDE(i, n) {
+    const int s = (int)(i / cols), c = (int)(i % cols);
+    out[i] = to_f(hidden[tiled ? tiled_act_offset(cu[s], c, cols) : (size_t)cu[s] * cols + c]);
+  }
+}
+
+// Row-major copy of a tiled activation matrix, one 16-byte chunk per thread.
+template <typename T>
+__global__ void untile_kernel(const T* in, int64_t rows, int cols, T* out) {
+  constexpr int E = 16 / sizeof(T);
+  const int64_t n = rows * (cols / E);
+  FL_GRID_STRIDE(i, n) {
+    const int64_t r = i / (cols / E);
+    const int c = (int)(i % (cols / E)) * E;
+    *(u32x4_t*)(out + r * cols + c) = *(const u32x4_t*)(in + tiled_act_offset(r, c, cols));
   }
 }
 
@@ -370,25 +383,39 @@ hipError_t launch_rope(int dtype, void* t, int rows, int heads, int head_dim, in
 
 hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, const int* cu_seqlens,
                                    int nseq, int max_len, int l2, float* partial, float* out,
-                                   int* nan_flag, int rows_per_chunk, hipStream_t s) {
+                                   int* nan_flag, int rows_per_chunk, hipStream_t s,
+                                   bool tiled) {
   if (nseq <= 0) return hipSuccess;
+  if (tiled && (dtype == F32 || cols % 32)) return hipErrorInvalidValue;
   const int max_chunks = (max_len + rows_per_chunk - 1) / rows_per_chunk;
   dim3 g1(max_chunks, nseq);
   const int threads = cols >= 256 ? 256 : 64;
   FL_DISPATCH(dtype, T, hipLaunchKernelGGL(pool_partial_kernel<T>, g1, dim3(threads), 0, s,
                                            (const T*)hidden, cols, cu_seqlens, rows_per_chunk,
-                                           max_chunks, partial));
+                                           max_chunks, partial, tiled));
   hipLaunchKernelGGL(pool_final_kernel, dim3(nseq), dim3(256), 0, s, partial, cols, cu_seqlens,
                      rows_per_chunk, max_chunks, l2, out, nan_flag);
   return hipGetLastError();
 }
 
 hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,
-                             int nseq, float* out, hipStream_t s) {
+                             int nseq, float* out, hipStream_t s, bool tiled) {
   const int64_t total = (int64_t)nseq * cols;
   if (total <= 0) return hipSuccess;
+  if (tiled && (dtype == F32 || cols % 32)) return hipErrorInvalidValue;
   FL_DISPATCH(dtype, T, hipLaunchKernelGGL(gather_cls_kernel<T>, grid_for(total), dim3(256), 0, s,
-                                           (const T*)hidden, cols, cu_seqlens, nseq, out));
+                                           (const T*)hidden, cols, cu_seqlens, nseq, out, tiled));
+  return hipGetLastError();
+}
+
+hipError_t launch_untile(int dtype, const void* in, int64_t rows, int cols, void* out,
+                         hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (dtype == F32 || cols % 32 || (((uintptr_t)in | (uintptr_t)out) & 15))
+    return hipErrorInvalidValue;
+  const int64_t total = rows * (cols / 8);
+  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(untile_kernel<T>, grid_for(total), dim3(256), 0, s,
+                                           (const T*)in, rows, cols, (T*)out));
   return hipGetLastError();
 }
 

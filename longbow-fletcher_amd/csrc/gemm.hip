@@ -11,6 +11,7 @@
 // features of one token: stores are 8/16-byte vectors and the RoPE pair
 // (j, j+32) and the SwiGLU (gate, up) pair land in the same lane.
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1212,6 +1213,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     const int mrow = m0 + wm * 128 + r;
     const int cbase = n0 + wn * 128;  // the wave's first packed feature
     char* stg = lds + NS * STAGE + wave * 8192;
+    const int mlast = p.epi.c_padded ? INT_MAX : p.M - 1;
     float4_t bv[2][4];
     if constexpr (HB) {
 #pragma unroll
@@ -1285,9 +1287,10 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       for (int k = 0; k < CPRW / 4; ++k) {
         const int rr = ln / CPRW + k * (64 / CPRW);
         const u32x4_t val = *(const u32x4_t*)(buf + rr * RB + ((c ^ (rr % CPRW)) << 4));
-        // Rows past M hold row M-1's outputs (computed from its inputs) and
-        // are stored there again: the same bytes, and no branch.
-        const int m = min(m0 + wm * 128 + t * 16 + rr, p.M - 1);
+        // Rows past M go to their own padding rows (c_padded), or else hold
+        // row M-1's outputs (computed from its inputs) and are stored there
+        // again: the same bytes.  Either way, no branch.
+        const int m = min(m0 + wm * 128 + t * 16 + rr, mlast);
         *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + col0 + c * 8) = val;
       }
     };
@@ -1459,7 +1462,7 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     if (p.epi.layout >= PACK_LANE16) {
       if constexpr (pp_epilogue_ok(EPI, MATH)) {
         if (gemm_w4_ok(p)) return launch_w4<T, EPI, MATH>(p, s);
-        if (p.epi.out_tiled || p.epi.a_tiled) return hipErrorInvalidValue;
+        if (p.epi.out_tiled || p.epi.a_tiled || p.epi.c_padded) return hipErrorInvalidValue;
         return launch_pp<T, EPI, MATH>(p, s);
       }
       return hipErrorInvalidValue;
@@ -1505,12 +1508,11 @@ int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bia
 }
 
 bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
-                   bool a_tiled) {
-  if (!out_tiled && !a_tiled) return true;
+                   bool a_tiled, bool c_padded) {
+  if (!out_tiled && !a_tiled && !c_padded) return true;
   if (gemm_pp_layout(dtype, N, K, epi_kind, math, has_bias) < 0 || !gemm_w4_shape_ok(K))
     return false;
   if (out_tiled && (epi_kind != EPI_SWIGLU || (N / 2) % 32)) return false;
-  if (a_tiled && epi_kind != EPI_STORE) return false;
   return true;
 }
 
@@ -1518,7 +1520,7 @@ bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, c
                        int ldb, const void* C, int ldc, const GemmEpilogue& epi) {
   if (M <= 0 || N <= 0 || K <= 0) return false;
   if (!gemm_tiled_ok(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr, epi.out_tiled,
-                     epi.a_tiled))
+                     epi.a_tiled, epi.c_padded))
     return false;
   if (epi.layout >= PACK_LANE16) {
     if (gemm_pp_layout(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr) != epi.layout)

@@ -93,6 +93,11 @@ struct GemmEpilogue {
   // rows like any other.
   bool out_tiled = false;
   bool a_tiled = false;
+  // C has rows up to the next multiple of 256: rows past M are written to
+  // their own rows instead of row M-1.  Without it, the rows of A past M
+  // must be copies of row M-1 (true of row-major A, which is read clamped,
+  // and of a tiled output written by an out_tiled GEMM from such an A).
+  bool c_padded = false;
 };
 
 // Element offset of (row m, column k) of an activation matrix with K columns
@@ -104,9 +109,9 @@ __host__ __device__ inline size_t tiled_act_offset(int64_t m, int k, int K) {
 
 // Whether the tiled-activation options can be used for this GEMM (the
 // four-wave kernel takes it): 16-bit, ping-pong layout, K % 128 == 0,
-// K >= 256; out_tiled only with the SwiGLU epilogue, a_tiled only with STORE.
+// K >= 256; out_tiled only with the SwiGLU epilogue.
 bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
-                   bool a_tiled);
+                   bool a_tiled, bool c_padded);
 
 // The packing the ping-pong GEMM needs for this problem, or -1 when that
 // kernel does not take it (the caller then packs PACK_PLAIN / PACK_SWIGLU16
@@ -168,15 +173,17 @@ hipError_t launch_attention_generic(int dtype, const void* q, const void* k, con
 
 // ---- normalisation / embedding ---------------------------------------------
 // t = LN(t [+ residual]) row-wise, fp32 statistics; gamma/beta fp32.
+// t_tiled: t is stored tiled (tiled_act_offset; 16-bit, cols % 256 == 0,
+// cols <= 1024), the residual row-major.
 hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
                             const float* gamma, const float* beta, float eps,
-                            hipStream_t stream);
+                            hipStream_t stream, bool t_tiled = false);
 // x[t] = LN(word[ids[t]] + pos[pos_ids[t]] (if pos) + type[0]).  Ids outside
 // [0, vocab) read row 0 and set *bad_id (never an out-of-bounds read).
 hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,
                            const void* pos_table, const void* type_table, int T, int H,
                            const float* gamma, const float* beta, float eps, int vocab,
-                           int* bad_id, void* out, hipStream_t stream);
+                           int* bad_id, void* out, hipStream_t stream, bool out_tiled = false);
 
 // ---- elementwise ------------------------------------------------------------
 hipError_t launch_add(int dtype, void* t, const void* o, int64_t n, hipStream_t s);
@@ -200,12 +207,16 @@ hipError_t launch_rope(int dtype, void* t, int rows, int heads, int head_dim, in
 // scratch of nseq * ceil(max_len / rows_per_chunk) * cols floats.
 hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, const int* cu_seqlens,
                                    int nseq, int max_len, int l2, float* partial, float* out,
-                                   int* nan_flag, int rows_per_chunk, hipStream_t s);
+                                   int* nan_flag, int rows_per_chunk, hipStream_t s,
+                                   bool tiled = false);
 // out[r, c] = silu(in[r, c]) * in[r, inter + c] over an unfused [rows, 2*inter] product.
 hipError_t launch_swiglu(int dtype, const void* in, int rows, int inter, void* out, int math,
                          hipStream_t s);
 // Gathers the first row of each sequence as fp32 [nseq x cols].
 hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,
-                             int nseq, float* out, hipStream_t s);
+                             int nseq, float* out, hipStream_t s, bool tiled = false);
+// Row-major copy of a tiled [rows, cols] activation matrix (tiled_act_offset).
+hipError_t launch_untile(int dtype, const void* in, int64_t rows, int cols, void* out,
+                         hipStream_t s);
 
 }  // namespace fl

@@ -98,6 +98,10 @@ struct fl_model {
   // The SwiGLU output (FFN-down's activations) is kept in the tiled layout
   // (tiled_act_offset), so FFN-down streams it in contiguous 16 KB blocks.
   bool ffn_tiled = false;
+  // The residual stream X (LayerNorm outputs, the QKV and FFN-up
+  // activations) is kept tiled too; activation buffers then have rows up to
+  // a multiple of 256 and the GEMMs reading X write their padding rows.
+  bool x_tiled = false;
   const float2* rope_cs = nullptr;
   const float2* rope_cs_q = nullptr;  // rope_cs * scale * log2(e), for a pre-scaled Q
 
@@ -198,7 +202,8 @@ int ensure_capacity(fl_model* m, int64_t T, int nseq, size_t nwork, size_t part_
     for (void* p : {m->X, m->QKV, m->CTX, m->TMP, m->G2, (void*)m->ids32, (void*)m->pos32})
       untrack_free(m, p);
     m->G2 = nullptr;
-    int64_t cap = std::max<int64_t>(T, 256);
+    // Rows rounded up to whole 256-row tiles (tiled activations, padded GEMM outputs).
+    int64_t cap = (std::max<int64_t>(T, 256) + 255) / 256 * 256;
     const int64_t wide = std::max<int64_t>(3 * m->H, m->Ni);
     M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->X));
     M_ST(track_alloc(m, (size_t)cap * wide * m->esz, &m->QKV));
@@ -344,7 +349,8 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
     ProfScope ps(m, P_EMBED);
     M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : m->pos32, m->word,
                             m->rope ? nullptr : m->pos, m->type, Ti, H, m->emb_g, m->emb_b,
-                            m->cfg.ln_eps, m->cfg.vocab_size, m->flags + 1, m->X, s));
+                            m->cfg.ln_eps, m->cfg.vocab_size, m->flags + 1, m->X, s,
+                            m->x_tiled));
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const LayerW& w = m->layers[l];
@@ -364,6 +370,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
         e.q_scale = attn_scale(m->hd) * kLog2e;
         e.rope_cs_q = m->rope_cs_q;
       }
+      e.a_tiled = e.c_padded = m->x_tiled;
       M_ST(gemm(m, m->mfma_qkv, m->X, w.wqkv, m->QKV, Ti, 3 * H, H, e));
       if (m->rope && !m->rope_fused)
         M_CHECK(launch_rope(dt, m->QKV, Ti, 2 * m->heads, m->hd, 3 * H, m->pos32, m->rope_cs, s));
@@ -394,7 +401,8 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
     }
     {
       ProfScope ps(m, P_LN);
-      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s));
+      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s,
+                               m->x_tiled));
     }
     {
       ProfScope ps(m, P_UP);
@@ -406,6 +414,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
         if (m->mfma_up) {
           e.kind = EPI_SWIGLU;
           e.out_tiled = m->ffn_tiled;
+          e.a_tiled = m->x_tiled;
           M_ST(gemm(m, true, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
         } else {
           // Unfused: [T, 2I] product, then silu(gate) * up into QKV.
@@ -423,25 +432,29 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       e.bias = w.bd;
       e.layout = m->lay_down;
       e.a_tiled = m->ffn_tiled;
+      // With X tiled, the SwiGLU output's padding rows come from X's padding
+      // rows (no copies of row T-1): FFN-down writes its own padding rows.
+      e.c_padded = m->x_tiled;
       M_ST(gemm(m, m->mfma_down, m->QKV, w.wd, m->TMP, Ti, H, m->I, e));
     }
     {
       ProfScope ps(m, P_LN);
-      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s));
+      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s,
+                               m->x_tiled));
     }
   }
   {
     ProfScope ps(m, P_POOL);
     if (m->cfg.pool == FL_POOL_CLS_TANH) {
       // BertPooler (bert.go:441-488) in fp32 (bert.go:459-476 forces fp32 for fp16 weights).
-      M_CHECK(launch_gather_cls(dt, m->X, H, m->cu, nseq, m->cls, s));
+      M_CHECK(launch_gather_cls(dt, m->X, H, m->cu, nseq, m->cls, s, m->x_tiled));
       M_CHECK(launch_gemm_generic(FL_F32, 0, 0, nseq, H, H, 1.0f, m->cls, H, m->pool_w, H, d_out,
                                   H, m->pool_b, FL_ACT_TANH, m->cfg.math, s));
       M_CHECK(launch_has_nan(d_out, FL_F32, (int64_t)nseq * H, m->flags, s));
     } else {
       M_CHECK(launch_mean_pool_staged(dt, m->X, H, m->cu, nseq, m->max_len,
                                       m->cfg.pool == FL_POOL_MEAN_L2, m->part, d_out, m->flags,
-                                      kPoolRows, s));
+                                      kPoolRows, s, m->x_tiled));
     }
   }
   return FL_OK;
@@ -505,8 +518,16 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
                      m->H % 64 == 0;
     m->ffn_tiled = FL_FFN_TILED && m->swiglu && m->lay_up == PACK_SWIGLU_LANE && m->lay_down >= PACK_LANE16 &&
-                   gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, false) &&
-                   gemm_tiled_ok(m->dtype, m->H, m->I, EPI_STORE, c.math, has_bias, false, true);
+                   gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, false,
+                                 false) &&
+                   gemm_tiled_ok(m->dtype, m->H, m->I, EPI_STORE, c.math, has_bias, false, true,
+                                 true);
+    const int qkv_kind = m->rope && m->rope_fused ? EPI_ROPE : EPI_STORE;
+    m->x_tiled = m->ffn_tiled && m->lay_qkv >= PACK_LANE16 && m->H % 256 == 0 && m->H <= 1024 &&
+                 gemm_tiled_ok(m->dtype, 3 * m->H, m->H, qkv_kind, c.math, has_bias, false, true,
+                               true) &&
+                 gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, true,
+                               false);
   }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
@@ -749,9 +770,16 @@ int fl_model_last_hidden(fl_model* m, float* out, int64_t n) {
   M_ST(activate(m->ctx));
   if (n != m->T * m->H) return fail(FL_ERR_INVALID, "size mismatch");
   int st;
-  void* tmp = workspace(m->ctx, (size_t)n * 4, &st);
+  // fp32 copy, then (X tiled) the row-major fp16 rows just past it.
+  void* tmp = workspace(m->ctx, (size_t)n * 4 + (m->x_tiled ? (size_t)n * m->esz : 0), &st);
   if (st) return st;
-  M_CHECK(launch_cast(m->X, m->dtype, tmp, FL_F32, n, 0, m->ctx->stream));
+  const void* x = m->X;
+  if (m->x_tiled) {
+    void* rm = (char*)tmp + (size_t)n * 4;
+    M_CHECK(launch_untile(m->dtype, m->X, m->T, m->H, rm, m->ctx->stream));
+    x = rm;
+  }
+  M_CHECK(launch_cast(x, m->dtype, tmp, FL_F32, n, 0, m->ctx->stream));
   M_CHECK(hipMemcpyAsync(out, tmp, (size_t)n * 4, hipMemcpyDeviceToHost, m->ctx->stream));
   M_CHECK(hipStreamSynchronize(m->ctx->stream));
   return FL_OK;

@@ -135,7 +135,10 @@ layernorm_kernel(T* t, const T* residual, int rows, int cols, const float* gamma
 // 16-byte vectors, LPR lanes per row (64 / LPR rows per wave): for H = 768
 // in 16 bits, half a wave per row and three 16-byte loads per lane and
 // tensor, so twice the rows per wave are in flight.
-template <typename T, int LPR, int NCH, int VEC>
+// TT: t is stored tiled (tiled_act_offset), 16-byte vectors never straddle
+// a tiled chunk; the two rows of a wave are adjacent, so each load of the
+// wave covers whole 128-byte lines of the tiled blocks.
+template <typename T, int LPR, int NCH, int VEC, bool TT>
 __global__ void __launch_bounds__(256)
 layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* gamma,
                       const float* beta, float eps) {
@@ -143,16 +146,18 @@ layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* 
   const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + ((threadIdx.x & 63) / LPR);
   const int lane = threadIdx.x % LPR;
   if (row >= rows) return;
-  T* tr = t + (size_t)row * cols;
   const T* rr = residual ? residual + (size_t)row * cols : nullptr;
   float x[NCH][VEC];
   bool valid[NCH];
   int col0[NCH];
+  auto tp = [&](int col) -> T* {
+    return TT ? t + tiled_act_offset(row, col, cols) : t + (size_t)row * cols + col;
+  };
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     col0[c] = (lane + c * LPR) * VEC;
     valid[c] = col0[c] < cols;
-    if (valid[c]) load_vec<T, VEC>(tr + col0[c], x[c]);
+    if (valid[c]) load_vec<T, VEC>(tp(col0[c]), x[c]);
   }
   if (rr) {
 #pragma unroll
@@ -167,16 +172,20 @@ layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* 
   ln_core<NCH, VEC, LPR>(x, valid, cols, gamma, beta, col0, eps);
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    if (valid[c]) store_vec<T, VEC>(tr + col0[c], x[c]);
+    if (valid[c]) store_vec<T, VEC>(tp(col0[c]), x[c]);
 }
 
 template <typename T, int LPR, int NCH, int VEC>
 static hipError_t ln_rows_launch(void* t, const void* res, int rows, int cols, const float* g,
-                                 const float* b, float eps, hipStream_t s) {
+                                 const float* b, float eps, hipStream_t s, bool tiled) {
   constexpr int rows_per_block = 4 * (64 / LPR);
-  hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC>),
-                     dim3((rows + rows_per_block - 1) / rows_per_block), dim3(256), 0, s, (T*)t,
-                     (const T*)res, rows, cols, g, b, eps);
+  const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+  if (tiled)
+    hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, true>), grid, dim3(256), 0, s,
+                       (T*)t, (const T*)res, rows, cols, g, b, eps);
+  else
+    hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, false>), grid, dim3(256), 0, s,
+                       (T*)t, (const T*)res, rows, cols, g, b, eps);
   return hipGetLastError();
 }
 
@@ -190,17 +199,18 @@ static hipError_t ln_launch(void* t, const void* res, int rows, int cols, const 
 
 template <typename T>
 static hipError_t ln_typed(void* t, const void* res, int rows, int cols, const float* g,
-                           const float* b, float eps, hipStream_t s) {
+                           const float* b, float eps, hipStream_t s, bool tiled) {
   constexpr int V16 = 16 / sizeof(T);  // elements per 16-byte vector
   if (cols % (32 * V16) == 0 && cols <= 4 * 32 * V16 &&
       (((uintptr_t)t | (uintptr_t)res) % 16) == 0) {
     switch (cols / (32 * V16)) {
-      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, rows, cols, g, b, eps, s);
-      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, rows, cols, g, b, eps, s);
-      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, rows, cols, g, b, eps, s);
-      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, rows, cols, g, b, eps, s);
+      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, rows, cols, g, b, eps, s, tiled);
+      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, rows, cols, g, b, eps, s, tiled);
+      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, rows, cols, g, b, eps, s, tiled);
+      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, rows, cols, g, b, eps, s, tiled);
     }
   }
+  if (tiled) return hipErrorInvalidValue;
   if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res) % (4 * sizeof(T)) == 0)) {
     const int nch = (cols / 4 + 63) / 64;
     if (nch <= 1) return ln_launch<T, 1, 4>(t, res, rows, cols, g, b, eps, s);
@@ -220,12 +230,13 @@ static hipError_t ln_typed(void* t, const void* res, int rows, int cols, const f
 
 hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
                             const float* gamma, const float* beta, float eps,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool t_tiled) {
   if (rows <= 0) return hipSuccess;
+  if (t_tiled && (dtype == F32 || cols % 256)) return hipErrorInvalidValue;
   switch (dtype) {
-    case F32: return ln_typed<float>(t, residual, rows, cols, gamma, beta, eps, stream);
-    case F16: return ln_typed<_Float16>(t, residual, rows, cols, gamma, beta, eps, stream);
-    case BF16: return ln_typed<__bf16>(t, residual, rows, cols, gamma, beta, eps, stream);
+    case F32: return ln_typed<float>(t, residual, rows, cols, gamma, beta, eps, stream, false);
+    case F16: return ln_typed<_Float16>(t, residual, rows, cols, gamma, beta, eps, stream, t_tiled);
+    case BF16: return ln_typed<__bf16>(t, residual, rows, cols, gamma, beta, eps, stream, t_tiled);
   }
   return hipErrorInvalidValue;
 }
@@ -234,7 +245,7 @@ hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, 
 // Fused embedding (BertEmbeddings.ForwardBatch, bert.go:215-261):
 // x = (word[id] + pos[p]) + type[0], then LayerNorm, one write.
 // ---------------------------------------------------------------------------
-template <typename T, int NCH, int VEC>
+template <typename T, int NCH, int VEC, bool OT>
 __global__ void __launch_bounds__(256)
 embed_ln_kernel(const int* ids, const int* pos_ids, const T* word, const T* pos_table,
                 const T* type_table, int rows, int cols, const float* gamma, const float* beta,
@@ -271,10 +282,13 @@ embed_ln_kernel(const int* ids, const int* pos_ids, const T* word, const T* pos_
     }
   }
   ln_core<NCH, VEC>(x, valid, cols, gamma, beta, col0, eps);
-  T* orow = out + (size_t)row * cols;
+  // OT: tiled output (tiled_act_offset); VEC elements never straddle a chunk.
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    if (valid[c]) store_vec<T, VEC>(orow + col0[c], x[c]);
+    if (valid[c])
+      store_vec<T, VEC>(OT ? out + tiled_act_offset(row, col0[c], cols)
+                           : out + (size_t)row * cols + col0[c],
+                        x[c]);
 }
 
 struct EmbArgs {
@@ -290,13 +304,21 @@ struct EmbArgs {
   int vocab;
   int* bad_id;
   void* out;
+  bool out_tiled;
 };
 
 template <typename T, int NCH, int VEC>
 static hipError_t emb_launch(const EmbArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((embed_ln_kernel<T, NCH, VEC>), dim3((a.T + 3) / 4), dim3(256), 0, s, a.ids,
-                     a.pos_ids, (const T*)a.word, (const T*)a.pos_table, (const T*)a.type_table,
-                     a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id, (T*)a.out);
+  if (a.out_tiled)
+    hipLaunchKernelGGL((embed_ln_kernel<T, NCH, VEC, true>), dim3((a.T + 3) / 4), dim3(256), 0, s,
+                       a.ids, a.pos_ids, (const T*)a.word, (const T*)a.pos_table,
+                       (const T*)a.type_table, a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id,
+                       (T*)a.out);
+  else
+    hipLaunchKernelGGL((embed_ln_kernel<T, NCH, VEC, false>), dim3((a.T + 3) / 4), dim3(256), 0,
+                       s, a.ids, a.pos_ids, (const T*)a.word, (const T*)a.pos_table,
+                       (const T*)a.type_table, a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id,
+                       (T*)a.out);
   return hipGetLastError();
 }
 
@@ -320,10 +342,11 @@ static hipError_t emb_typed(const EmbArgs& a, hipStream_t s) {
 hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,
                            const void* pos_table, const void* type_table, int T_, int H,
                            const float* gamma, const float* beta, float eps, int vocab,
-                           int* bad_id, void* out, hipStream_t stream) {
+                           int* bad_id, void* out, hipStream_t stream, bool out_tiled) {
   if (T_ <= 0) return hipSuccess;
+  if (out_tiled && (dtype == F32 || H % 256)) return hipErrorInvalidValue;
   const EmbArgs a{ids, pos_ids, word, pos_table, type_table, T_, H, gamma, beta, eps, vocab,
-                  bad_id, out};
+                  bad_id, out, out_tiled};
   switch (dtype) {
     case F32: return emb_typed<float>(a, stream);
     case F16: return emb_typed<_Float16>(a, stream);

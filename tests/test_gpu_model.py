@@ -228,3 +228,40 @@ def test_model_errors(ctx, fl):
             m.set_weight("q_w.0", np.zeros(5))                      # wrong size
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("pool", ["mean_l2", "cls"])
+def test_last_hidden_row_major(ctx, fl, orc, pool):
+    """The hidden states the library hands back are row-major whatever layout
+    the forward keeps them in (the 16-bit Nomic path keeps them tiled): the
+    pooled output must be the pooling of last_hidden, on a ragged batch whose
+    token count is not a multiple of 256.  The CLS pooler's input row (the
+    first of each sequence) is checked against the oracle's hidden state."""
+    cfg = synth.nomic(layers=2, max_pos=1024,
+                      pool=synth.POOL_MEAN_L2 if pool == "mean_l2" else synth.POOL_CLS_TANH)
+    lengths = np.array([1, 37, 300, 5, 129, 64, 255, 2, 90], np.int64)
+    ids = synth.make_ids(lengths)
+    T = int(lengths.sum())
+    assert T % 256
+    m = fl.Model(ctx, cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(weights_for(cfg))
+        out = m.forward(ids, lengths)
+        hid = m.last_hidden(T)
+    finally:
+        m.close()
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    if pool == "mean_l2":
+        want = np.stack([hid[s:s + L].astype(np.float64).mean(0)
+                         for s, L in zip(starts, lengths)])
+        want /= np.linalg.norm(want, axis=1, keepdims=True)
+        c = cosines(out, want)
+        log(f"last_hidden mean-pool min cos {c.min():.7f}")
+        assert c.min() >= 0.99999
+        np.testing.assert_allclose(out, want, atol=2e-4)
+    else:
+        w = weights_for(cfg)
+        x = hid[starts].astype(np.float64)
+        want = np.tanh(x @ np.asarray(w["pool_w"], np.float64).reshape(cfg.hidden, cfg.hidden)
+                       + np.asarray(w["pool_b"], np.float64))
+        np.testing.assert_allclose(out, want, atol=2e-3)
