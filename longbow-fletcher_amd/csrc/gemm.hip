@@ -1138,9 +1138,15 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // Prologue: steps 0 .. 3 into stages 0 .. 3; wait for steps 0 and 1;
   // fragments of step 0 into register set 0.
   load_tile(0);
+  if constexpr (EPI == EPI_ROPE) {
 #pragma unroll
-  for (int s = 0; s < NS; ++s) load_step(s);
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NLD) : "memory");
+    for (int s = 0; s < NS - 1; ++s) load_step(s);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NLD) : "memory");
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) load_step(s);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NLD) : "memory");
+  }
   asm volatile(FL_W4_READ_0 ::"v"(rdA), "v"(rdB) : "memory", FL_W4_CLOBBER_V);
 
   // K step j of a group of four (global step s = j mod 4, since every tile
@@ -1152,7 +1158,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // can let the epilogue's stores stay outstanding.
   auto kstep = [&](auto jc, auto zero, auto vmc) __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
-    constexpr bool Z = decltype(zero)::value;
+    constexpr int Z = decltype(zero)::value;  // 0 accumulate, 1 zero without DMA, 2 zero with DMA
     constexpr int VM = decltype(vmc)::value;
     constexpr uint32_t RD = ((J + 1) % NS) * STAGE, DM = ((J + NS - 1) % NS) * STAGE;
 #define FL_W4_ARGS                                                                          \
@@ -1161,18 +1167,22 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       "n"(VM)                                                                              \
   : "memory", "m0", "scc", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A
     if constexpr (F16T) {
-      if constexpr (J % 2 == 0 && !Z) asm volatile(FL_W4_STEP_F16_0_0 FL_W4_ARGS);
-      if constexpr (J % 2 == 0 && Z) asm volatile(FL_W4_STEP_F16_0_1 FL_W4_ARGS);
-      if constexpr (J % 2 == 1 && !Z) asm volatile(FL_W4_STEP_F16_1_0 FL_W4_ARGS);
-      if constexpr (J % 2 == 1 && Z) asm volatile(FL_W4_STEP_F16_1_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 0) asm volatile(FL_W4_STEP_F16_0_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 1) asm volatile(FL_W4_STEP_F16_0_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 2) asm volatile(FL_W4_STEP_F16_0_2 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 0) asm volatile(FL_W4_STEP_F16_1_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 1) asm volatile(FL_W4_STEP_F16_1_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 2) asm volatile(FL_W4_STEP_F16_1_2 FL_W4_ARGS);
     } else {
-      if constexpr (J % 2 == 0 && !Z) asm volatile(FL_W4_STEP_BF16_0_0 FL_W4_ARGS);
-      if constexpr (J % 2 == 0 && Z) asm volatile(FL_W4_STEP_BF16_0_1 FL_W4_ARGS);
-      if constexpr (J % 2 == 1 && !Z) asm volatile(FL_W4_STEP_BF16_1_0 FL_W4_ARGS);
-      if constexpr (J % 2 == 1 && Z) asm volatile(FL_W4_STEP_BF16_1_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 0) asm volatile(FL_W4_STEP_BF16_0_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 1) asm volatile(FL_W4_STEP_BF16_0_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 0 && Z == 2) asm volatile(FL_W4_STEP_BF16_0_2 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 0) asm volatile(FL_W4_STEP_BF16_1_0 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 1) asm volatile(FL_W4_STEP_BF16_1_1 FL_W4_ARGS);
+      if constexpr (J % 2 == 1 && Z == 2) asm volatile(FL_W4_STEP_BF16_1_2 FL_W4_ARGS);
     }
 #undef FL_W4_ARGS
-    if constexpr (!Z) {
+    if constexpr (Z != 1) {
       ka += KA_STEP;
       kb += KB_STEP;
     }
@@ -1238,13 +1248,23 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
         for (int k = 0; k < 4; ++k) cs[u % (RD + 1)][k] = src[k];
       }
     };
-    // Unit u is assembled in staging buffer u % 2 and stored while unit u+1
-    // is computed, so the LDS round trip of one overlaps the other's math.
+    // Unit u is assembled in an LDS buffer of 4 KB (ubuf) and stored from
+    // there.  STORE / SwiGLU: buffer u % 2, stored while unit u+1 is
+    // computed, so the LDS round trip of one overlaps the other's math.
+    // RoPE: six buffers (the staging area and this wave's 8 KB of stages 0
+    // and 3, both free during the epilogue); units 0-5 are computed before
+    // the first store, so every table load is issued ahead of every store.
     const int col0 = EPI == EPI_SWIGLU ? cbase / 2 : cbase;
+    auto ubuf = [&](int u) __attribute__((always_inline)) -> char* {
+      if constexpr (EPI != EPI_ROPE) return stg + (u & 1) * 4096;
+      const int b = u < 6 ? u : u - 6;
+      char* base = b < 2 ? stg : lds + (b < 4 ? 0 : 3) * STAGE + wave * 8192;
+      return base + (b & 1) * 4096;
+    };
     auto compute_unit = [&](auto uc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
-      char* buf = stg + (u & 1) * 4096;
+      char* buf = ubuf(u);
       fetch_cs(std::integral_constant<int, u + RD>{});
       auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
         const int c = (col - col0) >> 3;
@@ -1264,7 +1284,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     auto store_unit = [&](auto uc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
-      const char* buf = stg + (u & 1) * 4096;
+      const char* buf = ubuf(u);
       if constexpr (EPI == EPI_SWIGLU) {
         if (p.epi.out_tiled) {
           // Tiled output: the unit's 16 rows of each 32-column K slice are one
@@ -1294,15 +1314,32 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
         *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + col0 + c * 8) = val;
       }
     };
-    auto unit = [&](auto uc) __attribute__((always_inline)) {
-      constexpr int u = decltype(uc)::value;
-      compute_unit(uc);
-      if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{});
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
-    w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
-    store_unit(std::integral_constant<int, NUNITS - 1>{});
+    if constexpr (EPI == EPI_ROPE) {
+      // Every wave has read stage 0 (the next tile's first fragments).
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
+      w4_for<6>([&](auto uc) __attribute__((always_inline)) {
+        compute_unit(uc);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      store_unit(std::integral_constant<int, 0>{});
+      compute_unit(std::integral_constant<int, 6>{});
+      store_unit(std::integral_constant<int, 1>{});
+      compute_unit(std::integral_constant<int, 7>{});
+      w4_for<6>([&](auto uc) __attribute__((always_inline)) {
+        store_unit(std::integral_constant<int, decltype(uc)::value + 2>{});
+      });
+    } else {
+      auto unit = [&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        compute_unit(uc);
+        if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
+      w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
+      store_unit(std::integral_constant<int, NUNITS - 1>{});
+    }
     asm volatile("" ::: "memory");
   };
   auto epilogue = [&](int ti) __attribute__((always_inline)) {
@@ -1326,17 +1363,21 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   using VM8 = std::integral_constant<int, NLD>;
   using VME = std::integral_constant<int, NLD + EST>;
   using VM63 = std::integral_constant<int, 63>;
-  using Z1 = std::true_type;
-  using Z0 = std::false_type;
+  // RoPE keeps stage 3 free for its epilogue: the next tile's first step
+  // loads its step 3 itself, and its step 2 then waits for the stores.
+  constexpr bool PRE3 = EPI != EPI_ROPE;
+  using Z0 = std::integral_constant<int, 0>;
+  using ZF = std::integral_constant<int, PRE3 ? 1 : 2>;
+  using VM2 = std::conditional_t<PRE3, VME, VM8>;
   const int G4 = nk / 4;
   for (int ti = 0; ti < my_tiles; ++ti) {
-    kstep(I0{}, Z1{}, VM63{});
+    kstep(I0{}, ZF{}, VM63{});
     if (ti == 0) {
       kstep(I1{}, Z0{}, VM8{});
       kstep(I2{}, Z0{}, VM8{});
     } else {
       kstep(I1{}, Z0{}, VME{});
-      kstep(I2{}, Z0{}, VME{});
+      kstep(I2{}, Z0{}, VM2{});
     }
     kstep(I3{}, Z0{}, VM8{});
     for (int g = 1; g < G4 - 1; ++g) {
@@ -1353,7 +1394,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     // Steps 0 and 1 of the next tile have landed (step 1 is read in its
     // first step); step 3 goes out before the stores.
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
-    load_step(3);
+    if constexpr (PRE3) load_step(3);
     epilogue(ti);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
