@@ -41,6 +41,7 @@ typedef struct fl_model fl_model;
 #define FL_ERR_HIP 2         /* HIP runtime error */
 #define FL_ERR_OOM 3         /* device allocation failed */
 #define FL_ERR_UNSUPPORTED 4 /* valid request this backend does not implement */
+#define FL_ERR_IO 5          /* weight file missing, unreadable or malformed */
 
 /* device.DataType (device.go:119-124): Float32 = 0, Float16 = 1; BF16 added. */
 #define FL_F32 0
@@ -218,6 +219,15 @@ int fl_model_free(fl_model *model);
  * "out_ln_g.l" "out_ln_b.l" [H]; "pool_w" [H,H], "pool_b" [H].  Host fp32;
  * the backend converts and repacks for its kernels. */
 int fl_model_set_weight(fl_model *model, const char *name, const float *data, int64_t n);
+/* Loader.LoadFromRawBinary (weights/loader.go:29-90): every tensor of the
+ * model as little-endian float32 in the loader's fixed order, with the shapes
+ * NewBertModel allocates (position table and bias vectors included even where
+ * the model does not use them; a bias-free model requires them to be zero). */
+int fl_model_load_raw(fl_model *model, const char *path);
+/* Loader.LoadFromSafeTensors (weights/loader.go:155-237): F32 tensors by
+ * HuggingFace BERT name; 2-D linear ".weight" tensors are [out, in] and are
+ * transposed. */
+int fl_model_load_safetensors(fl_model *model, const char *path);
 /* ForwardBatch over flat host ids (sum(lengths)) and per-sequence lengths;
  * writes [nseq x hidden] fp32 to host `out` (synchronises). */
 int fl_model_forward(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,

@@ -14,6 +14,7 @@ module raises on use; there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import pathlib
 import re
 
@@ -25,7 +26,7 @@ PKG = pathlib.Path(__file__).resolve().parent
 LIB_PATH = PKG / "lib" / "libfletcher_hip.so"
 HEADER = PKG.parent / "include" / "fletcher_hip.h"
 
-OK, ERR_INVALID, ERR_HIP, ERR_OOM, ERR_UNSUPPORTED = 0, 1, 2, 3, 4
+OK, ERR_INVALID, ERR_HIP, ERR_OOM, ERR_UNSUPPORTED, ERR_IO = 0, 1, 2, 3, 4, 5
 F32, F16, BF16 = 0, 1, 2
 ACT_IDENTITY, ACT_GELU, ACT_TANH, ACT_SOFTMAX, ACT_SWIGLU = 0, 1, 2, 3, 4
 MATH_REFERENCE, MATH_EXACT = 0, 1
@@ -97,6 +98,8 @@ _SIGS = {
     "fl_model_create": ([_vp, C.POINTER(ModelConfigC), C.POINTER(_vp)], _i),
     "fl_model_free": ([_vp], _i),
     "fl_model_set_weight": ([_vp, _cp, _vp, _i64], _i),
+    "fl_model_load_raw": ([_vp, _cp], _i),
+    "fl_model_load_safetensors": ([_vp, _cp], _i),
     "fl_model_forward": ([_vp, _vp, _vp, _i, _vp], _i),
     "fl_model_forward_padded": ([_vp, _vp, _vp, _i, _i, _vp], _i),
     "fl_model_forward_device": ([_vp, _vp, _vp, _i, _vp], _i),
@@ -358,6 +361,16 @@ class Model:
     def load(self, weights: dict) -> "Model":
         for name, arr in weights.items():
             self.set_weight(name, arr)
+        return self
+
+    def load_raw(self, path) -> "Model":
+        """Loader.LoadFromRawBinary (weights/loader.go:29-90)."""
+        check(lib().fl_model_load_raw(self.h, os.fsencode(path)))
+        return self
+
+    def load_safetensors(self, path) -> "Model":
+        """Loader.LoadFromSafeTensors (weights/loader.go:155-237)."""
+        check(lib().fl_model_load_safetensors(self.h, os.fsencode(path)))
         return self
 
     def forward(self, ids, lengths) -> np.ndarray:

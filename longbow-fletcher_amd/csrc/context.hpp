@@ -50,6 +50,9 @@ namespace fl {
 
 inline size_t dtype_size(int dt) { return dt == FL_F32 ? 4 : 2; }
 
+// The configuration a model was created with.
+const fl_model_config* model_config(const fl_model* m);
+
 // Makes ctx current on the calling thread (cgo calls land on arbitrary OS threads).
 int activate(fl_context* ctx);
 // Returns scratch of at least `bytes` (synchronises the stream when it grows).

@@ -462,6 +462,8 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
 
 }  // namespace
 
+const fl_model_config* fl::model_config(const fl_model* m) { return &m->cfg; }
+
 extern "C" {
 
 int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out) {

@@ -178,6 +178,86 @@ def make_weights(cfg: ModelConfig, seed: int = 1234, std: float = 0.02) -> dict:
     return out
 
 
+def reference_tensor_order(cfg: ModelConfig):
+    """Every tensor of the reference model in weights/loader.go order
+    (LoadFromRawBinary :40-88, the same order LoadFromSafeTensors visits,
+    :199-236): (HF name, weight name used here, rows, cols, is_bias), with the
+    shapes NewBertModel allocates (bert.go:191-193, 279-280, 396-397,
+    542-547, 742-743, 776-777, 807-808).  The position table and the
+    projection biases (is_bias) are part of the file even for models that never
+    read them; the pooler's bias is used by every model."""
+    H, I, Ni = cfg.hidden, cfg.intermediate, cfg.inter_cols
+    out = [("embeddings.word_embeddings.weight", "word_emb", cfg.vocab_size, H, False),
+           ("embeddings.position_embeddings.weight", "pos_emb", cfg.max_pos, H, False),
+           ("embeddings.token_type_embeddings.weight", "type_emb", 2, H, False),
+           ("embeddings.LayerNorm.weight", "emb_ln_g", 1, H, False),
+           ("embeddings.LayerNorm.bias", "emb_ln_b", 1, H, False)]
+    for l in range(cfg.layers):
+        p = f"encoder.layer.{l}"
+        for hf, f in (("query", "q"), ("key", "k"), ("value", "v")):
+            out += [(f"{p}.attention.self.{hf}.weight", f"{f}_w.{l}", H, H, False),
+                    (f"{p}.attention.self.{hf}.bias", f"{f}_b.{l}", 1, H, True)]
+        out += [(f"{p}.attention.output.dense.weight", f"o_w.{l}", H, H, False),
+                (f"{p}.attention.output.dense.bias", f"o_b.{l}", 1, H, True),
+                (f"{p}.attention.output.LayerNorm.weight", f"attn_ln_g.{l}", 1, H, False),
+                (f"{p}.attention.output.LayerNorm.bias", f"attn_ln_b.{l}", 1, H, False),
+                (f"{p}.intermediate.dense.weight", f"inter_w.{l}", H, Ni, False),
+                (f"{p}.intermediate.dense.bias", f"inter_b.{l}", 1, Ni, True),
+                (f"{p}.output.dense.weight", f"out_w.{l}", I, H, False),
+                (f"{p}.output.dense.bias", f"out_b.{l}", 1, H, True),
+                (f"{p}.output.LayerNorm.weight", f"out_ln_g.{l}", 1, H, False),
+                (f"{p}.output.LayerNorm.bias", f"out_ln_b.{l}", 1, H, False)]
+    out += [("pooler.dense.weight", "pool_w", H, H, False),
+            ("pooler.dense.bias", "pool_b", 1, H, False)]
+    return out
+
+
+def _file_tensor(weights: dict, name: str, rows: int, cols: int) -> np.ndarray:
+    """The tensor as the reference stores it ([rows, cols] float32); tensors a
+    model does not have (RoPE position table, biases of bias-free models) are
+    written as zeros."""
+    a = weights.get(name)
+    if a is None:
+        return np.zeros((rows, cols), np.float32)
+    return np.ascontiguousarray(a, np.float32).reshape(rows, cols)
+
+
+def save_raw_binary(cfg: ModelConfig, weights: dict, path) -> None:
+    """Writes the file Loader.LoadFromRawBinary reads (weights/loader.go:29-90):
+    each tensor's float32 values little-endian, back to back, in loader order."""
+    with open(path, "wb") as f:
+        for _hf, name, rows, cols, _bias in reference_tensor_order(cfg):
+            f.write(_file_tensor(weights, name, rows, cols).astype("<f4").tobytes())
+
+
+def save_safetensors(cfg: ModelConfig, weights: dict, path) -> None:
+    """Writes F32 SafeTensors with the HF names Loader.LoadFromSafeTensors looks
+    up (weights/loader.go:199-236).  Linear weights are stored [out, in] (the HF
+    convention the loader transposes, :209-229); biases and LayerNorm vectors as
+    1-D, embedding tables as [rows, H]."""
+    import json
+    header, blobs, off = {}, [], 0
+    for hf, name, rows, cols, _bias in reference_tensor_order(cfg):
+        a = _file_tensor(weights, name, rows, cols)
+        linear = (hf.endswith(".weight") and rows > 1 and "embeddings" not in hf
+                  and "LayerNorm" not in hf)
+        if linear:
+            a = np.ascontiguousarray(a.T)
+        elif rows == 1:
+            a = a.reshape(cols)
+        b = a.astype("<f4").tobytes()
+        header[hf] = {"dtype": "F32", "shape": list(a.shape), "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    h = json.dumps(header, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little"))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
 def make_ids(lengths, seed: int = 4321, vocab_lo: int = 1000, vocab_hi: int = 30000) -> np.ndarray:
     """Flat int64 ids, [101] + uniform ids + [102] per sequence (length includes framing)."""
     lengths = np.asarray(lengths, dtype=np.int64)
