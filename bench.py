@@ -96,6 +96,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end (host ids in, pooled vectors out) measurement")
     ap.add_argument("--calibrate", action="store_true",
                     help="run one plain 256 MiB fp16 copy kernel first (reference for HBM counters)")
     a = ap.parse_args()
@@ -202,6 +204,30 @@ def main():
                         "traffic": traffic}
         log(json.dumps(kernels))
 
+    e2e = None
+    if not a.no_e2e:
+        # Host int64 ids in, host fp32 vectors out (PCIe included), with the
+        # reference's Linux GPU batching defaults: the pipelined entry point
+        # against one synchronous forward per batch of the same plan.
+        ms_, mt_ = 512, 16384
+        plan = fl.plan_batches(lengths, ms_, mt_)
+        starts = np.concatenate([[0], np.cumsum(lengths)])
+        model.embed(ids, lengths, ms_, mt_)
+        reps = max(1, min(5, a.steps))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            _o, _n, nb = model.embed(ids, lengths, ms_, mt_)
+        pipe_s = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for first, count in plan:
+                model.forward(ids[starts[first]:starts[first + count]], lengths[first:first + count])
+        seq_s = (time.perf_counter() - t0) / reps
+        e2e = {"max_seqs": ms_, "max_tokens": mt_, "batches": nb,
+               "pipelined_embeddings_per_s": round(len(lengths) / pipe_s, 1),
+               "sequential_embeddings_per_s": round(len(lengths) / seq_s, 1)}
+        log(f"end to end: {e2e}")
+
     cpu = None
     if not a.no_cpu_baseline:
         log("cpu baseline ...")
@@ -223,6 +249,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "end_to_end": e2e,
         "output_nan": nan, "bad_ids": bad,
     }
     print(json.dumps(out), flush=True)

@@ -241,6 +241,21 @@ int fl_model_forward_padded(fl_model *model, const int64_t *ids, const int64_t *
  * context stream. */
 int fl_model_forward_device(fl_model *model, const int32_t *d_ids, const int64_t *lengths,
                             int nseq, float *d_out);
+/* runInferenceOnDevice's batching loop (embeddings.go:690-775) in one call:
+ * sequences are taken in order into batches that end before the sequence
+ * that would pass max_seqs sequences or max_tokens tokens (a batch always
+ * holds at least one; the reference's Linux GPU defaults are 512 and 16384,
+ * embeddings.go:84-131), and each batch runs the model forward.  Ids go up
+ * and pooled vectors come back on copy streams while the next batch
+ * computes, replacing the reference's double-buffered outputs (:766-775).
+ * ids: flat host ids of all sequences (framing included, as in
+ * fl_model_forward); out: host fp32 [nseq x hidden] in input order;
+ * batch_nan (optional) int32 [nseq]: 1 where the sequence's batch output held
+ * a NaN/Inf (the per-batch HasNaN check, :757-764); nbatches (optional): the
+ * number of batches run.  Returns when every output is on the host. */
+int fl_model_embed(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
+                   int max_seqs, int64_t max_tokens, float *out, int32_t *batch_nan,
+                   int *nbatches);
 /* Tensor.HasNaN on the pooled output of the previous forward (computed inside
  * the pooling kernel, embeddings.go:757-764) and whether any id was outside
  * [0, vocab) (such ids read row 0).  Synchronises. */

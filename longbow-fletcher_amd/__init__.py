@@ -99,6 +99,7 @@ _SIGS = {
     "fl_model_free": ([_vp], _i),
     "fl_model_set_weight": ([_vp, _cp, _vp, _i64], _i),
     "fl_model_load_raw": ([_vp, _cp], _i),
+    "fl_model_embed": ([_vp, _vp, _vp, _i, _i, _i64, _vp, _vp, C.POINTER(_i)], _i),
     "fl_model_load_safetensors": ([_vp, _cp], _i),
     "fl_model_forward": ([_vp, _vp, _vp, _i, _vp], _i),
     "fl_model_forward_padded": ([_vp, _vp, _vp, _i, _i, _vp], _i),
@@ -336,6 +337,23 @@ class Context:
         return out
 
 
+def plan_batches(lengths, max_seqs: int = 512, max_tokens: int = 16384):
+    """The (first sequence, count) batches fl_model_embed runs: the batching
+    loop of runInferenceOnDevice (embeddings.go:704-731)."""
+    plan, i, n = [], 0, len(lengths)
+    while i < n:
+        size, tokens = 0, 0
+        for j in range(i, n):
+            if size >= max_seqs or (tokens + int(lengths[j]) > max_tokens and size > 0):
+                break
+            tokens += int(lengths[j])
+            size += 1
+        size = max(size, 1)
+        plan.append((i, size))
+        i += size
+    return plan
+
+
 class Model:
     """BertModel on the HIP backend (bert.go:77-169)."""
 
@@ -380,6 +398,20 @@ class Model:
         check(lib().fl_model_forward(self.h, ids.ctypes.data, lengths.ctypes.data, lengths.size,
                                      out.ctypes.data))
         return out
+
+    def embed(self, ids, lengths, max_seqs: int = 512, max_tokens: int = 16384):
+        """All sequences through token-budget batches with overlapped copies
+        (runInferenceOnDevice, embeddings.go:690-775).  Returns (pooled
+        [nseq, hidden] fp32, per-sequence NaN flag of its batch, batch count)."""
+        ids = np.ascontiguousarray(ids, np.int64)
+        lengths = np.ascontiguousarray(lengths, np.int64)
+        out = np.zeros((lengths.size, self.cfg.hidden), np.float32)
+        nan = np.zeros(lengths.size, np.int32)
+        nb = C.c_int()
+        check(lib().fl_model_embed(self.h, ids.ctypes.data, lengths.ctypes.data, lengths.size,
+                                   int(max_seqs), int(max_tokens), out.ctypes.data,
+                                   nan.ctypes.data, C.byref(nb)))
+        return out, nan.astype(bool), nb.value
 
     def forward_padded(self, ids, mask) -> np.ndarray:
         ids = np.ascontiguousarray(ids, np.int64)

@@ -90,6 +90,33 @@ struct fl_model {
   float* out = nullptr;
   int* flags = nullptr;  // [0] NaN in pooled output, [1] id out of range
 
+  // Pinned host staging of the per-batch metadata (attention work list,
+  // cu_seqlens, positions), two slots used in turn so a batch's upload never
+  // waits for the previous batch's kernels: a slot is refilled only after
+  // its copy (event) has completed.
+  struct Staging {
+    void* host = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+  } meta[2];
+  int meta_slot = 0;
+
+  // fl_model_embed's pipeline: ids go up on `up`, pooled vectors and the
+  // batch's flags come back on `down`, forwards run on the context stream.
+  struct Pipe {
+    hipStream_t up = nullptr, down = nullptr;
+    int32_t* ids_pin[2] = {nullptr, nullptr};
+    float* out_pin[2] = {nullptr, nullptr};
+    int* flags_pin[2] = {nullptr, nullptr};
+    int* ids_dev[2] = {nullptr, nullptr};
+    float* out_dev[2] = {nullptr, nullptr};
+    int* flags_dev[2] = {nullptr, nullptr};
+    hipEvent_t h2d[2] = {nullptr, nullptr}, fwd[2] = {nullptr, nullptr}, d2h[2] = {nullptr, nullptr};
+    int64_t cap_tok = 0;
+    int cap_seq = 0;
+  } pipe;
+
   std::vector<int64_t> last_lengths;
   int64_t T = 0;
   int n_work = 0, max_len = 0, waves = 4;
@@ -277,7 +304,28 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
   const bool same = (int)m->last_lengths.size() == nseq &&
                     std::equal(m->last_lengths.begin(), m->last_lengths.end(), lengths);
   if (!same) {
-    std::vector<int> cu(nseq + 1, 0), pos((size_t)T);
+    // Layout of a staging slot: work list (16-byte entries) | cu | pos.
+    const size_t need = nwork * sizeof(AttnWork) + (size_t)(nseq + 1) * 4 + (size_t)T * 4;
+    fl_model::Staging& sg = m->meta[m->meta_slot];
+    m->meta_slot ^= 1;
+    if (sg.pending) {
+      M_CHECK(hipEventSynchronize(sg.done));
+      sg.pending = false;
+    }
+    if (!sg.done) M_CHECK(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
+    if (sg.cap < need) {
+      if (sg.host) M_CHECK(hipHostFree(sg.host));
+      sg.host = nullptr;
+      sg.cap = 0;
+      const size_t cap = (need + (1 << 20) - 1) & ~(size_t)((1 << 20) - 1);
+      if (hipHostMalloc(&sg.host, cap, hipHostMallocDefault) != hipSuccess || !sg.host)
+        return fail(FL_ERR_OOM, "hipHostMalloc(batch metadata)");
+      sg.cap = cap;
+    }
+    AttnWork* work = (AttnWork*)sg.host;
+    int* cu = (int*)(work + nwork);
+    int* pos = cu + nseq + 1;
+    cu[0] = 0;
     for (int b = 0; b < nseq; ++b) {
       cu[b + 1] = cu[b] + (int)lengths[b];
       for (int i = 0; i < (int)lengths[b]; ++i) {
@@ -286,8 +334,7 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
         pos[cu[b] + i] = m->rope ? i : std::min(i, m->cfg.max_pos - 1);
       }
     }
-    std::vector<AttnWork> work;
-    work.reserve(nwork);
+    size_t n_work = 0;
     if (fast_attn) {
       std::vector<int> order(nseq);
       for (int b = 0; b < nseq; ++b) order[b] = b;
@@ -295,7 +342,7 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
                        [&](int a, int b) { return lengths[a] > lengths[b]; });
       for (int b : order)
         for (int h = 0; h < m->heads; ++h)
-          for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work.push_back(AttnWork{b, h, q0, 0});
+          for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work[n_work++] = AttnWork{b, h, q0, 0};
     }
     if (m->rope) {
       int st;
@@ -307,15 +354,17 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
         if (st) return st;
       }
     }
+    // Stream-ordered after the previous batch's kernels, which read the same
+    // device buffers.
     hipStream_t s = m->ctx->stream;
-    M_CHECK(hipMemcpyAsync(m->cu, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, s));
-    M_CHECK(hipMemcpyAsync(m->pos32, pos.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
-    if (!work.empty())
-      M_CHECK(hipMemcpyAsync(m->work, work.data(), work.size() * sizeof(AttnWork),
-                             hipMemcpyHostToDevice, s));
-    M_CHECK(hipStreamSynchronize(s));
+    M_CHECK(hipMemcpyAsync(m->cu, cu, (nseq + 1) * 4, hipMemcpyHostToDevice, s));
+    M_CHECK(hipMemcpyAsync(m->pos32, pos, (size_t)T * 4, hipMemcpyHostToDevice, s));
+    if (n_work)
+      M_CHECK(hipMemcpyAsync(m->work, work, n_work * sizeof(AttnWork), hipMemcpyHostToDevice, s));
+    M_CHECK(hipEventRecord(sg.done, s));
+    sg.pending = true;
     m->last_lengths.assign(lengths, lengths + nseq);
-    m->n_work = (int)work.size();
+    m->n_work = (int)n_work;
     m->waves = waves;
     m->qblocks = (max_len + bq - 1) / bq;
   }
@@ -339,17 +388,17 @@ int gemm(fl_model* m, bool mfma, const void* A, const void* W, void* C, int M, i
 }
 
 // The forward on device-resident ids (m->ids32 or caller memory) into d_out.
-int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
+int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
   hipStream_t s = m->ctx->stream;
   const int64_t T = m->T;
   const int H = m->H, dt = m->dtype;
   const int Ti = (int)T;
-  M_CHECK(hipMemsetAsync(m->flags, 0, 8, s));
+  M_CHECK(hipMemsetAsync(flags, 0, 8, s));
   {
     ProfScope ps(m, P_EMBED);
     M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : m->pos32, m->word,
                             m->rope ? nullptr : m->pos, m->type, Ti, H, m->emb_g, m->emb_b,
-                            m->cfg.ln_eps, m->cfg.vocab_size, m->flags + 1, m->X, s,
+                            m->cfg.ln_eps, m->cfg.vocab_size, flags + 1, m->X, s,
                             m->x_tiled));
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -450,10 +499,10 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out) {
       M_CHECK(launch_gather_cls(dt, m->X, H, m->cu, nseq, m->cls, s, m->x_tiled));
       M_CHECK(launch_gemm_generic(FL_F32, 0, 0, nseq, H, H, 1.0f, m->cls, H, m->pool_w, H, d_out,
                                   H, m->pool_b, FL_ACT_TANH, m->cfg.math, s));
-      M_CHECK(launch_has_nan(d_out, FL_F32, (int64_t)nseq * H, m->flags, s));
+      M_CHECK(launch_has_nan(d_out, FL_F32, (int64_t)nseq * H, flags, s));
     } else {
       M_CHECK(launch_mean_pool_staged(dt, m->X, H, m->cu, nseq, m->max_len,
-                                      m->cfg.pool == FL_POOL_MEAN_L2, m->part, d_out, m->flags,
+                                      m->cfg.pool == FL_POOL_MEAN_L2, m->part, d_out, flags,
                                       kPoolRows, s, m->x_tiled));
     }
   }
@@ -584,6 +633,17 @@ int fl_model_free(fl_model* m) {
     std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
     (void)activate(m->ctx);
     (void)hipStreamSynchronize(m->ctx->stream);
+    fl_model::Pipe& P = m->pipe;
+    for (hipStream_t st : {P.up, P.down})
+      if (st) (void)hipStreamSynchronize(st);
+    for (int k = 0; k < 2; ++k) {
+      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k], m->meta[k].host})
+        if (h) (void)hipHostFree(h);
+      for (hipEvent_t e : {P.h2d[k], P.fwd[k], P.d2h[k], m->meta[k].done})
+        if (e) (void)hipEventDestroy(e);
+    }
+    for (hipStream_t st : {P.up, P.down})
+      if (st) (void)hipStreamDestroy(st);
     for (void* p : m->owned) (void)hipFree(p);
     for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
   }
@@ -700,7 +760,7 @@ static int forward_common(fl_model* m, const int64_t* ids, const int64_t* length
   }
   hipStream_t s = m->ctx->stream;
   M_CHECK(hipMemcpyAsync(m->ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
-  M_ST(run(m, m->ids32, nseq, m->out));
+  M_ST(run(m, m->ids32, nseq, m->out, m->flags));
   M_CHECK(hipMemcpyAsync(out, m->out, (size_t)nseq * m->H * 4, hipMemcpyDeviceToHost, s));
   M_CHECK(hipStreamSynchronize(s));
   return FL_OK;
@@ -751,7 +811,125 @@ int fl_model_forward_device(fl_model* m, const int32_t* d_ids, const int64_t* le
   M_ST(activate(m->ctx));
   if (nseq == 0) return FL_OK;
   M_ST(prepare(m, lengths, nseq));
-  return run(m, d_ids, nseq, d_out);
+  return run(m, d_ids, nseq, d_out, m->flags);
+}
+
+int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq, int max_seqs,
+                   int64_t max_tokens, float* out, int32_t* batch_nan, int* nbatches) {
+  if (!m || (nseq > 0 && (!ids || !lengths || !out))) return fail(FL_ERR_INVALID, "null argument");
+  if (nseq < 0) return fail(FL_ERR_INVALID, "negative batch");
+  std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
+  M_ST(activate(m->ctx));
+  if (nbatches) *nbatches = 0;
+  if (nseq == 0) return FL_OK;
+  // embeddings.go:704-731: sequences in order; a batch ends before the
+  // sequence that would pass max_seqs sequences or max_tokens tokens, but
+  // always holds at least one sequence.
+  struct Batch { int first, count; int64_t tok0, tokens; };
+  std::vector<Batch> plan;
+  int64_t tok = 0, max_bt = 0;
+  int max_bs = 0;
+  for (int i = 0; i < nseq;) {
+    int count = 0;
+    int64_t tokens = 0;
+    for (int j = i; j < nseq; ++j) {
+      if (lengths[j] <= 0) return fail(FL_ERR_INVALID, "sequence lengths must be positive");
+      if (count >= max_seqs) break;
+      if (tokens + lengths[j] > max_tokens && count > 0) break;
+      tokens += lengths[j];
+      ++count;
+    }
+    if (count == 0) {
+      count = 1;
+      tokens = lengths[i];
+    }
+    plan.push_back({i, count, tok, tokens});
+    max_bt = std::max(max_bt, tokens);
+    max_bs = std::max(max_bs, count);
+    tok += tokens;
+    i += count;
+  }
+  for (int64_t t = 0; t < tok; ++t)
+    if (ids[t] < 0 || ids[t] >= m->cfg.vocab_size)  // cpu_backend.go:500-502
+      return fail(FL_ERR_INVALID, "Gather index out of bounds");
+
+  fl_model::Pipe& P = m->pipe;
+  hipStream_t cs = m->ctx->stream;
+  if (!P.up) {
+    M_CHECK(hipStreamCreateWithFlags(&P.up, hipStreamNonBlocking));
+    M_CHECK(hipStreamCreateWithFlags(&P.down, hipStreamNonBlocking));
+    for (int k = 0; k < 2; ++k)
+      for (hipEvent_t* e : {&P.h2d[k], &P.fwd[k], &P.d2h[k]})
+        M_CHECK(hipEventCreateWithFlags(e, hipEventDisableTiming));
+  }
+  if (max_bt > P.cap_tok || max_bs > P.cap_seq) {
+    M_CHECK(hipStreamSynchronize(cs));
+    M_CHECK(hipStreamSynchronize(P.up));
+    M_CHECK(hipStreamSynchronize(P.down));
+    const int64_t ct = std::max(max_bt, P.cap_tok);
+    const int cq = std::max(max_bs, P.cap_seq);
+    for (int k = 0; k < 2; ++k) {
+      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
+        if (h) M_CHECK(hipHostFree(h));
+      P.ids_pin[k] = nullptr;
+      P.out_pin[k] = nullptr;
+      P.flags_pin[k] = nullptr;
+      for (void* d : {(void*)P.ids_dev[k], (void*)P.out_dev[k], (void*)P.flags_dev[k]}) untrack_free(m, d);
+      if (hipHostMalloc((void**)&P.ids_pin[k], (size_t)ct * 4, hipHostMallocDefault) != hipSuccess ||
+          hipHostMalloc((void**)&P.out_pin[k], (size_t)cq * m->H * 4, hipHostMallocDefault) != hipSuccess ||
+          hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess) {
+        P.cap_tok = P.cap_seq = 0;
+        return fail(FL_ERR_OOM, "hipHostMalloc(embed pipeline)");
+      }
+      void* d;
+      M_ST(track_alloc(m, (size_t)ct * 4, &d));
+      P.ids_dev[k] = (int*)d;
+      M_ST(track_alloc(m, (size_t)cq * m->H * 4, &d));
+      P.out_dev[k] = (float*)d;
+      M_ST(track_alloc(m, 8, &d));
+      P.flags_dev[k] = (int*)d;
+    }
+    P.cap_tok = ct;
+    P.cap_seq = cq;
+  }
+
+  // Batch b uses slot b & 1.  The host fills a slot's pinned ids only after
+  // that slot's previous batch has been copied back (so its upload is long
+  // done too), and copies results out of it at the same point: the host runs
+  // up to two batches ahead of the device, like the reference's double
+  // buffering of outputs (embeddings.go:766-775).
+  const int64_t H = m->H;
+  auto drain = [&](int b) -> int {
+    const Batch& pb = plan[(size_t)b];
+    const int k = b & 1;
+    M_CHECK(hipEventSynchronize(P.d2h[k]));
+    std::memcpy(out + (size_t)pb.first * H, P.out_pin[k], (size_t)pb.count * H * 4);
+    if (batch_nan)
+      for (int i = 0; i < pb.count; ++i) batch_nan[pb.first + i] = P.flags_pin[k][0] != 0;
+    return FL_OK;
+  };
+  const int nb = (int)plan.size();
+  for (int b = 0; b < nb; ++b) {
+    const Batch& pb = plan[(size_t)b];
+    const int k = b & 1;
+    if (b >= 2) M_ST(drain(b - 2));
+    for (int64_t t = 0; t < pb.tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[pb.tok0 + t];
+    M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)pb.tokens * 4, hipMemcpyHostToDevice, P.up));
+    M_CHECK(hipEventRecord(P.h2d[k], P.up));
+    M_CHECK(hipStreamWaitEvent(cs, P.h2d[k], 0));
+    M_ST(prepare(m, lengths + pb.first, pb.count));
+    M_ST(run(m, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
+    M_CHECK(hipEventRecord(P.fwd[k], cs));
+    M_CHECK(hipStreamWaitEvent(P.down, P.fwd[k], 0));
+    M_CHECK(hipMemcpyAsync(P.out_pin[k], P.out_dev[k], (size_t)pb.count * H * 4, hipMemcpyDeviceToHost, P.down));
+    M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, P.down));
+    M_CHECK(hipEventRecord(P.d2h[k], P.down));
+  }
+  for (int b = std::max(0, nb - 2); b < nb; ++b) M_ST(drain(b));
+  // fl_model_status then reports the last batch.
+  M_CHECK(hipMemcpyAsync(m->flags, P.flags_dev[(nb - 1) & 1], 8, hipMemcpyDeviceToDevice, cs));
+  if (nbatches) *nbatches = nb;
+  return FL_OK;
 }
 
 int fl_model_status(fl_model* m, int* nan_in_output, int* bad_ids) {
