@@ -640,7 +640,8 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
     cu[b + 1] = cu[b] + (int)lengths[b];
     max_len = (int)lengths[b] > max_len ? (int)lengths[b] : max_len;
   }
-  const bool fast16 = (dtype == FL_F16 || dtype == FL_BF16) && hd == 64 && math == FL_MATH_EXACT &&
+  const bool fast16 = (dtype == FL_F16 || dtype == FL_BF16) && (hd == 64 || hd == 32) &&
+                      math == FL_MATH_EXACT &&
                       hidden % 8 == 0 && (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0 &&
                       ((uintptr_t)out & 7) == 0;
   const bool fast32 = dtype == FL_F32 && hd == 64 && hidden % 4 == 0 &&
@@ -669,7 +670,7 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
   const AttnWork* dwork = (const AttnWork*)(ws + cu_bytes);
   if (fast16) {
     FL_CHECK_LAUNCH(launch_attention_flash(dtype, q, k, v, hidden, out, hidden, dcu, dwork,
-                                           (int)work.size(), scale, waves, false,
+                                           (int)work.size(), hd, scale, waves, false,
                                            (max_len + bq - 1) / bq, ctx->stream));
   } else if (fast32) {
     FL_CHECK_LAUNCH(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, hidden,

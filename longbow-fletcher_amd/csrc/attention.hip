@@ -75,17 +75,23 @@ __device__ inline float quad_max(float v) {
 
 // One workgroup = WAVES waves x 32 query rows of one (sequence, head); key /
 // value tiles of 64 rows are double-buffered in LDS.  A tile is 64 rows of
-// 128 bytes; 16-byte chunk c of row r sits at chunk c ^ (r & 7).
+// D * 2 bytes (CH = D / 8 chunks of 16 bytes); chunk c of row r sits at
+// chunk c ^ (r % CH).  Head sizes 64 (BERT-base, Nomic) and 32 (MiniLM).
 //
 // Scores are kept relative to a running row maximum m in the exp2 domain:
 // x = s * scale * log2(e) - m, p = exp2(x).  PRE: Q arrives multiplied by
 // scale * log2(e) (the encoder's QKV epilogue does it), so the first score
 // MFMA starts from the accumulator -m and produces x directly; otherwise x
 // takes one FMA per score.
-template <typename T, int WAVES, bool PRE>
+template <typename T, int D, int WAVES, bool PRE>
 __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
-  constexpr int D = 64, BKV = 64, NT = WAVES * 64;
-  constexpr int TILE = BKV * D * 2;     // bytes of one K or V tile
+  static_assert(D == 32 || D == 64, "head size 32 or 64");
+  constexpr int BKV = 64, NT = WAVES * 64;
+  constexpr int ROWB = D * 2;           // bytes of one key / value row of a head
+  constexpr int CH = D / 8;             // 16-byte chunks per row
+  constexpr int DS = D / 32;            // 32-wide slices of d (score MFMA steps)
+  constexpr int DT = D / 16;            // 16-wide output tiles
+  constexpr int TILE = BKV * ROWB;      // bytes of one K or V tile
   constexpr int NLD = TILE / 16 / NT;   // 16-byte DMA loads per thread per tensor
   static_assert(TILE % (16 * NT) == 0, "tile/thread mismatch");
   // Rescale the running output only when a row max grows by more than
@@ -106,14 +112,14 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   const T* K = (const T*)p.k;
   const T* V = (const T*)p.v;
 
-  // Q fragments: [q-tile][d-half]; lane holds 8 consecutive d of one query.
+  // Q fragments: [q-tile][d-slice]; lane holds 8 consecutive d of one query.
   const int qbase = w.q0 + wave * 32;
-  u32x4_t qf[2][2];
+  u32x4_t qf[2][DS];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qr = qbase + qt * 16 + lr;
 #pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
+    for (int ds = 0; ds < DS; ++ds) {
       if (qr < L)
         qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + g * 8);
       else
@@ -122,15 +128,15 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   }
 
   // DMA: load j of this thread fills LDS chunk j*NT + tid, i.e. row
-  // (j*NT + tid) / 8, holding global chunk (tid % 8) ^ (row & 7).  In the
+  // (j*NT + tid) / CH, holding global chunk (tid % CH) ^ (row % CH).  In the
   // last tile, rows past the sequence re-read its last key (their scores are
   // masked to -inf, so their probabilities are exactly 0).
   const size_t ldk = (size_t)p.ld;
   size_t goff[NLD];
 #pragma unroll
   for (int j = 0; j < NLD; ++j) {
-    const int row = (j * NT + tid) >> 3;
-    goff[j] = (size_t)(s0 + row) * ldk + hoff + (((tid & 7) ^ (row & 7)) << 3);
+    const int row = (j * NT + tid) / CH;
+    goff[j] = (size_t)(s0 + row) * ldk + hoff + (((tid & (CH - 1)) ^ (row & (CH - 1))) << 3);
   }
   auto issue = [&](int kv0, int buf) __attribute__((always_inline)) {
     const bool tail = kv0 + BKV > L;
@@ -138,7 +144,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     for (int j = 0; j < NLD; ++j) {
       size_t off = goff[j] + (size_t)kv0 * ldk;
       if (tail) {
-        const int row = (j * NT + tid) >> 3;
+        const int row = (j * NT + tid) / CH;
         off -= (size_t)max(kv0 + row - (L - 1), 0) * ldk;
       }
       lds_char* kd = (lds_char*)&lds[buf][0][(j * NT + wave * 64) * 16];
@@ -151,22 +157,22 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   };
 
   // K fragment (S^T A operand): row kt*16 + lr, chunk ds*4 + g.
-  int koff[2];
+  int koff[DS];
 #pragma unroll
-  for (int ds = 0; ds < 2; ++ds) koff[ds] = lr * 128 + (((ds * 4 + g) ^ (lr & 7)) << 4);
+  for (int ds = 0; ds < DS; ++ds) koff[ds] = lr * ROWB + (((ds * 4 + g) ^ (lr & (CH - 1))) << 4);
   // V^T fragment (O^T A operand), transposing read: lane (g, s = lr) names
   // row 4g + s/4 (+16 for keys 16..31 of a 32-key step), bytes
   // [dt*32 + 8*(s%4), +8) of that row.
   const int vrow = 4 * g + (lr >> 2);
-  const int vx = ((lr & 3) >> 1) ^ (vrow & 7);
-  const int vbase = vrow * 128 + (lr & 1) * 8;
+  const int vx = ((lr & 3) >> 1) ^ (vrow & (CH - 1));
+  const int vbase = vrow * ROWB + (lr & 1) * 8;
 
-  float4_t o[4][2], lacc[2];
+  float4_t o[DT][2], lacc[2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     lacc[qt] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) o[dt][qt] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
   // Running row max m (exp2 domain); 0 until the first tile sets it.
   float ms[2] = {0.f, 0.f};
@@ -195,8 +201,8 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       s[kt][0] = PRE ? cinit[0] : float4_t{0.f, 0.f, 0.f, 0.f};
       s[kt][1] = PRE ? cinit[1] : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ds = 0; ds < 2; ++ds) {
-        const u32x4_t kf = *(const u32x4_t*)(kt_lds + kt * 2048 + koff[ds]);
+      for (int ds = 0; ds < DS; ++ds) {
+        const u32x4_t kf = *(const u32x4_t*)(kt_lds + kt * 16 * ROWB + koff[ds]);
         AttnMfma<T>::mma(s[kt][0], kf, qf[0][ds]);
         AttnMfma<T>::mma(s[kt][1], kf, qf[1][ds]);
       }
@@ -215,18 +221,19 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     // i/4 + 4j, j = 0..3.  Written as asm because the compiler cannot tell
     // these reads from the DMA into the other buffer and would wait for it;
     // the s_waitcnt before the P V MFMAs covers their completion.
-    u32x2_t vr[4][4];  // [dt][ks*2 + half]
+    u32x2_t vr[DT][4];  // [dt][ks*2 + half]
     const uint32_t vb = (uint32_t)(uintptr_t)(const lds_char*)vt_lds + vbase;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
       const uint32_t a = vb + (((dt * 2) ^ vx) << 4);
+      // Key rows +16, +32, +48 (the swizzle repeats every CH rows).
       asm volatile(
           "ds_read_b64_tr_b16 %0, %4\n"
-          "ds_read_b64_tr_b16 %1, %4 offset:2048\n"
-          "ds_read_b64_tr_b16 %2, %4 offset:4096\n"
-          "ds_read_b64_tr_b16 %3, %4 offset:6144\n"
+          "ds_read_b64_tr_b16 %1, %4 offset:%5\n"
+          "ds_read_b64_tr_b16 %2, %4 offset:%6\n"
+          "ds_read_b64_tr_b16 %3, %4 offset:%7\n"
           : "=&v"(vr[dt][0]), "=&v"(vr[dt][1]), "=&v"(vr[dt][2]), "=&v"(vr[dt][3])
-          : "v"(a));
+          : "v"(a), "n"(16 * ROWB), "n"(32 * ROWB), "n"(48 * ROWB));
     }
     if (kv0 + BKV > L) {
 #pragma unroll
@@ -265,7 +272,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
           const float alpha = __builtin_amdgcn_exp2f(-shift);
           lacc[qt] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) o[dt][qt] *= alpha;
+          for (int dt = 0; dt < DT; ++dt) o[dt][qt] *= alpha;
         }
       }
     }
@@ -291,17 +298,23 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 
     // O^T += V^T P^T; the row sums ride along as ones * P^T.
     {
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
-                     "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]),
-                     "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[2][2]), "+v"(vr[2][3]),
-                     "+v"(vr[3][0]), "+v"(vr[3][1]), "+v"(vr[3][2]), "+v"(vr[3][3]));
+      if constexpr (DT == 4) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
+                       "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]),
+                       "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[2][2]), "+v"(vr[2][3]),
+                       "+v"(vr[3][0]), "+v"(vr[3][1]), "+v"(vr[3][2]), "+v"(vr[3][3]));
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
+                       "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]));
+      }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
         AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
           const u32x2_t lo = vr[dt][ks * 2], hi = vr[dt][ks * 2 + 1];
           const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
           AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
@@ -322,7 +335,7 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     if (qr >= L) continue;
     T* orow = out + (size_t)(s0 + qr) * p.ldo + hoff + g * 4;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
       V4 h;
 #pragma unroll
       for (int i = 0; i < 4; ++i) h[i] = (T)(o[dt][qt][i] * inv);
@@ -332,27 +345,34 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 }
 
 template <typename T>
-static void launch_flash_typed(const AttnParams& p, int n_work, int waves, bool prescaled,
-                               hipStream_t stream) {
+static void launch_flash_typed(const AttnParams& p, int n_work, int head_dim, int waves,
+                               bool prescaled, hipStream_t stream) {
   const dim3 grid(n_work);
-  if (waves == 2) {
-    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 2, true>), grid, dim3(128), 0, stream, p);
-    else hipLaunchKernelGGL((attn_flash_kernel<T, 2, false>), grid, dim3(128), 0, stream, p);
+  if (head_dim == 32) {
+    // Only the unscaled form: the encoder pre-scales Q for head size 64 only.
+    if (waves == 2) hipLaunchKernelGGL((attn_flash_kernel<T, 32, 2, false>), grid, dim3(128), 0, stream, p);
+    else hipLaunchKernelGGL((attn_flash_kernel<T, 32, 4, false>), grid, dim3(256), 0, stream, p);
+  } else if (waves == 2) {
+    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 64, 2, true>), grid, dim3(128), 0, stream, p);
+    else hipLaunchKernelGGL((attn_flash_kernel<T, 64, 2, false>), grid, dim3(128), 0, stream, p);
   } else {
-    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 4, true>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((attn_flash_kernel<T, 4, false>), grid, dim3(256), 0, stream, p);
+    if (prescaled) hipLaunchKernelGGL((attn_flash_kernel<T, 64, 4, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((attn_flash_kernel<T, 64, 4, false>), grid, dim3(256), 0, stream, p);
   }
 }
 
 hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
-                                  const AttnWork* work, int n_work, float scale, int waves,
-                                  bool q_prescaled, int xcd_group_size, hipStream_t stream) {
+                                  const AttnWork* work, int n_work, int head_dim, float scale,
+                                  int waves, bool q_prescaled, int xcd_group_size,
+                                  hipStream_t stream) {
   if (n_work <= 0) return hipSuccess;
+  if ((head_dim != 32 && head_dim != 64) || (head_dim == 32 && q_prescaled))
+    return hipErrorInvalidValue;
   const AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale,
                      std::max(1, std::min(xcd_group_size, 32))};
-  if (dtype == F16) launch_flash_typed<_Float16>(p, n_work, waves, q_prescaled, stream);
-  else if (dtype == BF16) launch_flash_typed<__bf16>(p, n_work, waves, q_prescaled, stream);
+  if (dtype == F16) launch_flash_typed<_Float16>(p, n_work, head_dim, waves, q_prescaled, stream);
+  else if (dtype == BF16) launch_flash_typed<__bf16>(p, n_work, head_dim, waves, q_prescaled, stream);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

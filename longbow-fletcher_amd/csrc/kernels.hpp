@@ -151,14 +151,15 @@ struct AttnWork {
   int q0;      // first query row (relative to the sequence start)
   int pad;
 };
-// Flash attention (exact math, online softmax) for head_dim 64, 16-bit types.
-// q_prescaled: Q already holds q * scale * log2(e) (GemmEpilogue::q_scale).
-// xcd_group_size: consecutive work items (the query blocks of one sequence
-// and head) kept on one XCD, clamped to [1, 32].
+// Flash attention (exact math, online softmax) for head_dim 32 or 64, 16-bit
+// types.  q_prescaled (head_dim 64 only): Q already holds q * scale * log2(e)
+// (GemmEpilogue::q_scale).  xcd_group_size: consecutive work items (the query
+// blocks of one sequence and head) kept on one XCD, clamped to [1, 32].
 hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
-                                  const AttnWork* work, int n_work, float scale, int waves,
-                                  bool q_prescaled, int xcd_group_size, hipStream_t stream);
+                                  const AttnWork* work, int n_work, int head_dim, float scale,
+                                  int waves, bool q_prescaled, int xcd_group_size,
+                                  hipStream_t stream);
 // Two-pass attention (exact row max, then reference ExpFast or exp) for
 // head_dim 64 fp32.
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v, int ldqkv,

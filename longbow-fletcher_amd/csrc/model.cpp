@@ -292,7 +292,8 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
     max_len = std::max<int>(max_len, (int)lengths[b]);
   }
   if (T >= (int64_t)1 << 31) return fail(FL_ERR_INVALID, "too many tokens");
-  const bool fast_attn = m->hd == 64;
+  // Flash kernels: 16-bit head sizes 32 and 64; fp32 head size 64.
+  const bool fast_attn = m->hd == 64 || (m->hd == 32 && m->dtype != FL_F32);
   const int waves = max_len > 64 ? 4 : 2;
   const int bq = m->dtype == FL_F32 ? 64 : waves * 32;
   size_t nwork = 0;
@@ -430,9 +431,9 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
       const char* q = (const char*)m->QKV;
       const void* k = q + (size_t)H * m->esz;
       const void* v = q + (size_t)2 * H * m->esz;
-      if (m->hd == 64 && dt != FL_F32)
+      if ((m->hd == 64 || m->hd == 32) && dt != FL_F32)
         M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, m->CTX, H, m->cu, m->work, m->n_work,
-                                       scale, m->waves, m->q_prescaled, m->qblocks, s));
+                                       m->hd, scale, m->waves, m->q_prescaled, m->qblocks, s));
       else if (m->hd == 64)
         M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
                                      (float*)m->CTX, H, m->cu, m->work, m->n_work, scale,

@@ -123,6 +123,16 @@ def bert_base(**kw) -> ModelConfig:
     return ModelConfig(**base)
 
 
+def minilm(**kw) -> ModelConfig:
+    """DefaultMiniLMConfig (bert.go:62-75): all-MiniLM-L6-v2, head size 32.
+    The reference's LayerNorm ignores the config's eps (bert.go:281), so 1e-7
+    here too; pooled with mean + L2 like the other embedding workloads."""
+    base = dict(name="minilm", hidden=384, layers=6, heads=12, intermediate=1536,
+                max_pos=512, activation=ACT_GELU, position=POS_ABSOLUTE, pool=POOL_MEAN_L2)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
 def nomic(**kw) -> ModelConfig:
     """DefaultNomicConfig (bert.go:48-60) with BASELINE's RoPE base 1000,
     no biases, masked mean-pool + L2."""
@@ -298,4 +308,6 @@ WORKLOADS = {
     "nomic-b256-s512-f16": Workload("nomic-b256-s512-f16", nomic(), 256, 512, F16),
     "nomic-ragged-b512-f16": Workload("nomic-ragged-b512-f16", nomic(), 512, 512, F16, ragged=True),
     "nomic-b16-s8192-f16": Workload("nomic-b16-s8192-f16", nomic(), 16, 8192, F16),
+    # The reference's third model family (not a BASELINE configuration).
+    "minilm-b256-s128-f16": Workload("minilm-b256-s128-f16", minilm(), 256, 128, F16),
 }

@@ -194,6 +194,32 @@ def test_bf16_model(ctx, fl, orc):
     assert cosines(got, want).min() >= 0.995
 
 
+def test_minilm_f32_reference_math(ctx, fl, orc):
+    """The reference's MiniLM family (bert.go:62-75; head size 32) in fp32 with
+    reference math, whole batch against the oracle at the fp32 bar."""
+    cfg = synth.minilm()
+    lengths = np.array([128, 77, 5, 128, 33], np.int64)
+    ids = synth.make_ids(lengths)
+    got = run_gpu(fl, ctx, cfg, fl.F32, fl.MATH_REFERENCE, ids, lengths)
+    want = orc.forward(cfg, weights_for(cfg), ids, lengths)
+    c = cosines(got, want)
+    err = np.abs(got - want).max()
+    log(f"minilm f32 min cos {c.min():.9f} max abs {err:.3e}")
+    assert c.min() >= COS_F32 and err <= MAXABS_F32
+
+
+def test_minilm_f16(ctx, fl, orc):
+    w = synth.WORKLOADS["minilm-b256-s128-f16"]
+    lengths = w.lengths()
+    ids = synth.make_ids(lengths)
+    got = run_gpu(fl, ctx, w.cfg, fl.F16, fl.MATH_EXACT, ids, lengths)
+    rows = sample_rows(lengths, 4)
+    want = oracle_rows(orc, w.cfg, ids, lengths, rows)
+    c = cosines(got[rows], want)
+    log(f"minilm f16 min cos {c.min():.6f}")
+    assert c.min() >= COS_F16
+
+
 def test_forward_device_matches_host(ctx, fl):
     cfg = synth.bert_tiny()
     lengths = np.array([16, 9, 30], np.int64)

@@ -356,20 +356,22 @@ def test_attention_f32_reference_math(ctx, fl, orc, seq):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("seq", [512, 100, 1, 65])
-def test_attention_flash_16bit(ctx, fl, orc, dtype, seq):
+@pytest.mark.parametrize("hd", [64, 32, 48])  # flash kernel for 64 / 32, generic for 48
+def test_attention_flash_16bit(ctx, fl, orc, dtype, seq, hd):
     dt = fl.F16 if dtype == "f16" else fl.BF16
     b, heads = 2, 3
-    q, k, v = (rand(b * seq, heads * 64) for _ in range(3))
+    scale = 1.0 / math.sqrt(hd)
+    q, k, v = (rand(b * seq, heads * hd) for _ in range(3))
     dq, dk, dv = ctx.tensor(q, dt), ctx.tensor(k, dt), ctx.tensor(v, dt)
     qr, kr, vr = dq.numpy(), dk.numpy(), dv.numpy()
     want = np.zeros_like(qr, dtype=np.float64)
     for bi in range(b):
         for h in range(heads):
-            rs, cs = slice(bi * seq, (bi + 1) * seq), slice(h * 64, (h + 1) * 64)
-            s = qr[rs, cs].astype(np.float64) @ kr[rs, cs].astype(np.float64).T * 0.125
+            rs, cs = slice(bi * seq, (bi + 1) * seq), slice(h * hd, (h + 1) * hd)
+            s = qr[rs, cs].astype(np.float64) @ kr[rs, cs].astype(np.float64).T * scale
             p = np.exp(s - s.max(1, keepdims=True))
             want[rs, cs] = (p / p.sum(1, keepdims=True)) @ vr[rs, cs]
-    got = ctx.attention(dq, dk, dv, b, seq, heads, 0.125, fl.MATH_EXACT).numpy()
+    got = ctx.attention(dq, dk, dv, b, seq, heads, scale, fl.MATH_EXACT).numpy()
     tol = 4e-3 if dt == fl.F16 else 3e-2
     close(got, want, tol, tol)
 
