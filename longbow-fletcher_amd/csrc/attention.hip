@@ -73,6 +73,22 @@ __device__ inline float quad_max(float v) {
   return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
 }
 
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One 1 KB DMA load: 64 lanes x 16 bytes from gsrc + voff into LDS at lds_dst
+// (m0); gsrc and lds_dst are wave-uniform.  The flash kernel's own code never
+// uses m0.
+__device__ __attribute__((always_inline)) inline void attn_dma(uint32_t lds_dst, uint32_t voff,
+                                                               const void* gsrc) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2" ::"s"(lds_dst),
+      "v"(voff), "s"(gsrc)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // One workgroup = WAVES waves x 32 query rows of one (sequence, head); key /
 // value tiles of 64 rows are double-buffered in LDS.  A tile is 64 rows of
 // D * 2 bytes (CH = D / 8 chunks of 16 bytes); chunk c of row r sits at
@@ -131,28 +147,34 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   // (j*NT + tid) / CH, holding global chunk (tid % CH) ^ (row % CH).  In the
   // last tile, rows past the sequence re-read its last key (their scores are
   // masked to -inf, so their probabilities are exactly 0).
+  // Lane byte offsets from the sequence's first row (rows < 64 of a head, so
+  // 32 bits suffice); the tile's row offset rides in the 64-bit scalar base
+  // (global_load_lds with an SGPR base), so a tile's loads need no 64-bit
+  // lane arithmetic.
   const size_t ldk = (size_t)p.ld;
-  size_t goff[NLD];
+  uint32_t voff[NLD];
 #pragma unroll
   for (int j = 0; j < NLD; ++j) {
     const int row = (j * NT + tid) / CH;
-    goff[j] = (size_t)(s0 + row) * ldk + hoff + (((tid & (CH - 1)) ^ (row & (CH - 1))) << 3);
+    voff[j] = (uint32_t)(((size_t)row * ldk + hoff + (((tid & (CH - 1)) ^ (row & (CH - 1))) << 3)) *
+                         sizeof(T));
   }
+  const char* kseq = (const char*)(K + (size_t)s0 * ldk);
+  const char* vseq = (const char*)(V + (size_t)s0 * ldk);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)&lds[0][0][0];
   auto issue = [&](int kv0, int buf) __attribute__((always_inline)) {
     const bool tail = kv0 + BKV > L;
+    const size_t tb = (size_t)kv0 * ldk * sizeof(T);
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
-      size_t off = goff[j] + (size_t)kv0 * ldk;
+      uint32_t o = voff[j];
       if (tail) {
         const int row = (j * NT + tid) / CH;
-        off -= (size_t)max(kv0 + row - (L - 1), 0) * ldk;
+        o -= (uint32_t)((size_t)max(kv0 + row - (L - 1), 0) * ldk * sizeof(T));
       }
-      lds_char* kd = (lds_char*)&lds[buf][0][(j * NT + wave * 64) * 16];
-      lds_char* vd = (lds_char*)&lds[buf][1][(j * NT + wave * 64) * 16];
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(K + off),
-                                       (__attribute__((address_space(3))) void*)kd, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(V + off),
-                                       (__attribute__((address_space(3))) void*)vd, 16, 0, 0);
+      const uint32_t kd = lds_base + (uint32_t)((buf * 2) * TILE + (j * NT + wave * 64) * 16);
+      attn_dma(kd, o, kseq + tb);
+      attn_dma(kd + TILE, o, vseq + tb);
     }
   };
 
