@@ -537,8 +537,10 @@ __device__ inline void store8(T* dst, float4_t a, float4_t b) {
 // the (cos, sin) float4 k of the row's position in the group's RoPE table
 // (asked for every group; ignored past rope_cols).  The results go out
 // through put(col, a, b): eight outputs of the lane's row starting at output
-// column col.
-template <typename T, int EPI, int MATH, bool BIAS, typename BiasAt, typename RopeAt, typename Put>
+// column col.  ROT = false: the RoPE layout's columns without the rotation
+// (a group wholly past rope_cols; rope_at is not called).
+template <typename T, int EPI, int MATH, bool BIAS, bool ROT = true, typename BiasAt,
+          typename RopeAt, typename Put>
 __device__ __attribute__((always_inline)) inline void pp_epilogue_block(
     const GemmParams& p, float4_t (&v)[4], int nbase, int lane, BiasAt&& bias_at,
     RopeAt&& rope_at, Put&& put) {
@@ -563,7 +565,7 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue_block(
     // unchanged; the code stays free of branches.
     const bool rot = nbase < p.epi.rope_cols;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
+    for (int f = 0; f < 2 && ROT; ++f) {
 #pragma clang fp contract(off)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -1261,11 +1263,14 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       char* base = b < 2 ? stg : lds + (b < 4 ? 0 : 3) * STAGE + wave * 8192;
       return base + (b & 1) * 4096;
     };
-    auto compute_unit = [&](auto uc) __attribute__((always_inline)) {
+    // rotc = false (RoPE kernel, a wave wholly past rope_cols): two staging
+    // buffers and no tables, as for STORE.
+    auto compute_unit = [&](auto uc, auto rotc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
-      char* buf = ubuf(u);
-      fetch_cs(std::integral_constant<int, u + RD>{});
+      constexpr bool ROT = decltype(rotc)::value;
+      char* buf = ROT ? ubuf(u) : stg + (u & 1) * 4096;
+      if constexpr (ROT) fetch_cs(std::integral_constant<int, u + RD>{});
       auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
         const int c = (col - col0) >> 3;
         *(u32x4_t*)(buf + r * RB + ((c ^ (r % CPRW)) << 4)) = pack8<T>(a, b);
@@ -1274,17 +1279,17 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
         constexpr int h = decltype(hc)::value;
         float4_t v[4] = {W4Acc<(4 * h + 0) * 8 + t>::read(), W4Acc<(4 * h + 1) * 8 + t>::read(),
                          W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
-        pp_epilogue_block<T, EPI, MATH, HB>(
+        pp_epilogue_block<T, EPI, MATH, HB, ROT>(
             p, v, cbase + h * 64, ln, [&](int f) { return bv[h][f]; },
             [&](int k) { return cs[u % (RD + 1)][k]; }, put);
       };
       block(I0{});
       block(I1{});
     };
-    auto store_unit = [&](auto uc) __attribute__((always_inline)) {
+    auto store_unit = [&](auto uc, auto rotc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
-      const char* buf = ubuf(u);
+      const char* buf = decltype(rotc)::value ? ubuf(u) : stg + (u & 1) * 4096;
       if constexpr (EPI == EPI_SWIGLU) {
         if (p.epi.out_tiled) {
           // Tiled output: the unit's 16 rows of each 32-column K slice are one
@@ -1317,28 +1322,41 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     if constexpr (EPI == EPI_ROPE) {
       // Every wave has read stage 0 (the next tile's first fragments).
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (EPI == EPI_ROPE && cbase >= p.epi.rope_cols) {
+      // V columns: the STORE schedule (the same EST stores, no table loads).
+      using NR = std::false_type;
+      auto unit = [&](auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        compute_unit(uc, NR{});
+        if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{}, NR{});
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
+      store_unit(std::integral_constant<int, NUNITS - 1>{}, NR{});
+    } else if constexpr (EPI == EPI_ROPE) {
       w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
       w4_for<6>([&](auto uc) __attribute__((always_inline)) {
-        compute_unit(uc);
+        compute_unit(uc, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
       });
-      store_unit(std::integral_constant<int, 0>{});
-      compute_unit(std::integral_constant<int, 6>{});
-      store_unit(std::integral_constant<int, 1>{});
-      compute_unit(std::integral_constant<int, 7>{});
+      store_unit(std::integral_constant<int, 0>{}, std::true_type{});
+      compute_unit(std::integral_constant<int, 6>{}, std::true_type{});
+      store_unit(std::integral_constant<int, 1>{}, std::true_type{});
+      compute_unit(std::integral_constant<int, 7>{}, std::true_type{});
       w4_for<6>([&](auto uc) __attribute__((always_inline)) {
-        store_unit(std::integral_constant<int, decltype(uc)::value + 2>{});
+        store_unit(std::integral_constant<int, decltype(uc)::value + 2>{}, std::true_type{});
       });
     } else {
       auto unit = [&](auto uc) __attribute__((always_inline)) {
         constexpr int u = decltype(uc)::value;
-        compute_unit(uc);
-        if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{});
+        compute_unit(uc, std::true_type{});
+        if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{}, std::true_type{});
         __builtin_amdgcn_sched_barrier(0);
       };
       w4_for<RD>([&](auto uc) __attribute__((always_inline)) { fetch_cs(uc); });
       w4_for<NUNITS>([&](auto uc) __attribute__((always_inline)) { unit(uc); });
-      store_unit(std::integral_constant<int, NUNITS - 1>{});
+      store_unit(std::integral_constant<int, NUNITS - 1>{}, std::true_type{});
     }
     asm volatile("" ::: "memory");
   };
