@@ -98,16 +98,14 @@ __device__ inline float gelu_ref(float x) {
 
 __device__ inline float tanh_exact(float x) { return tanhf(x); }
 
-// tanh(y) = 1 - 2 / (exp(2y) + 1) on the hardware exp2 / reciprocal:
-// absolute error ~1e-7, which is what GELU's 0.5 x (1 + tanh) needs (the
-// stand-alone tanh activation keeps the libm function).
-__device__ inline float tanh_abs_fast(float y) {
-  const float e = __expf(2.0f * y);
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-}
-
+// 0.5 x (1 + tanh(y)) = x / (1 + exp(-2y)), y = sqrt(2/pi) (x + 0.044715 x^3):
+// with -2y log2(e) = x (k1 + k2 x^2) it is five VALU operations and two
+// transcendentals (exp2, reciprocal).  Large |x| saturate to x and -0.
 __device__ inline float gelu_exact(float x) {
-  return 0.5f * x * (1.0f + tanh_abs_fast(0.7978845608f * (x + 0.044715f * x * x * x)));
+  constexpr float k1 = -2.0f * 0.7978845608f * 1.4426950409f;
+  constexpr float k2 = k1 * 0.044715f;
+  const float q = x * __builtin_fmaf(x * x, k2, k1);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(q));
 }
 
 template <int MATH> __device__ inline float gelu_m(float x) {

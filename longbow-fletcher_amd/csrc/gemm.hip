@@ -1467,7 +1467,8 @@ static int cu_count() {
 // reference-formula SiLU) need more registers than it leaves next to its
 // accumulators and take the 4-wave kernels; so does RoPE with a bias.
 constexpr bool pp_epilogue_ok(int epi, int math) {
-  return epi == EPI_STORE || epi == EPI_ROPE || (math == MATH_EXACT && epi == EPI_SWIGLU);
+  return epi == EPI_STORE || epi == EPI_ROPE ||
+         (math == MATH_EXACT && (epi == EPI_SWIGLU || epi == EPI_GELU));
 }
 
 template <typename T, int EPI, int MATH>
