@@ -183,6 +183,46 @@ pool_partial_kernel(const T* hidden, int cols, const int* cu, int rows_per_chunk
   }
 }
 
+// Stage 1 with 16-byte loads: the workgroup's RL x CV work items are (row
+// lane, 16-byte column vector); row lane l sums rows r0 + l, r0 + l + RL, ...
+// of its vector, and the RL partial sums are added in a fixed order through
+// LDS (deterministic).  red holds RL x cols floats.
+template <typename T>
+__global__ void __launch_bounds__(256)
+pool_partial_vec_kernel(const T* hidden, int cols, const int* cu, int rows_per_chunk,
+                        int max_chunks, int RL, float* part, bool tiled) {
+  constexpr int VE = 16 / (int)sizeof(T);
+  using V = T __attribute__((ext_vector_type(VE)));
+  extern __shared__ float red[];
+  const int seq = blockIdx.y, chunk = blockIdx.x;
+  const int s0 = cu[seq], L = cu[seq + 1] - s0;
+  const int r0 = chunk * rows_per_chunk;
+  const int r1 = min(L, r0 + rows_per_chunk);
+  const int CV = cols / VE;
+  for (int it = threadIdx.x; it < RL * CV; it += blockDim.x) {
+    const int rl = it / CV, c = (it % CV) * VE;
+    float acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.f;
+#pragma unroll 4
+    for (int r = r0 + rl; r < r1; r += RL) {
+      const size_t off = tiled ? tiled_act_offset(s0 + r, c, cols) : (size_t)(s0 + r) * cols + c;
+      const V v = *(const V*)(hidden + off);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) acc[i] += to_f(v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VE; ++i) red[rl * cols + c + i] = acc[i];
+  }
+  __syncthreads();
+  float* dst = part + ((size_t)seq * max_chunks + chunk) * cols;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    float sum = 0.f;
+    for (int l = 0; l < RL; ++l) sum += red[l * cols + c];
+    dst[c] = sum;
+  }
+}
+
 // Stage 2: sum chunks, divide by L, optional L2 normalisation, NaN flag.
 __global__ void __launch_bounds__(256)
 pool_final_kernel(const float* part, int cols, const int* cu, int rows_per_chunk, int max_chunks,
@@ -389,10 +429,20 @@ hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, cons
   if (tiled && (dtype == F32 || cols % 32)) return hipErrorInvalidValue;
   const int max_chunks = (max_len + rows_per_chunk - 1) / rows_per_chunk;
   dim3 g1(max_chunks, nseq);
-  const int threads = cols >= 256 ? 256 : 64;
-  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(pool_partial_kernel<T>, g1, dim3(threads), 0, s,
-                                           (const T*)hidden, cols, cu_seqlens, rows_per_chunk,
-                                           max_chunks, partial, tiled));
+  const int ve = dtype == F32 ? 4 : 8;  // elements per 16-byte vector
+  const int cv = cols / ve;
+  const int rl = cv > 0 ? std::max(1, 256 / cv) : 1;
+  const size_t lds = (size_t)rl * cols * sizeof(float);
+  if (cols % ve == 0 && ((uintptr_t)hidden & 15) == 0 && lds <= 32768) {
+    FL_DISPATCH(dtype, T, hipLaunchKernelGGL(pool_partial_vec_kernel<T>, g1, dim3(256), lds, s,
+                                             (const T*)hidden, cols, cu_seqlens, rows_per_chunk,
+                                             max_chunks, rl, partial, tiled));
+  } else {
+    const int threads = cols >= 256 ? 256 : 64;
+    FL_DISPATCH(dtype, T, hipLaunchKernelGGL(pool_partial_kernel<T>, g1, dim3(threads), 0, s,
+                                             (const T*)hidden, cols, cu_seqlens, rows_per_chunk,
+                                             max_chunks, partial, tiled));
+  }
   hipLaunchKernelGGL(pool_final_kernel, dim3(nseq), dim3(256), 0, s, partial, cols, cu_seqlens,
                      rows_per_chunk, max_chunks, l2, out, nan_flag);
   return hipGetLastError();
