@@ -431,9 +431,11 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
       const char* q = (const char*)m->QKV;
       const void* k = q + (size_t)H * m->esz;
       const void* v = q + (size_t)2 * H * m->esz;
+      // XCD groups of two (sequence, head) pairs' query blocks: measured 2%
+      // faster than one pair at 512 tokens (the kernel clamps groups at 32).
       if ((m->hd == 64 || m->hd == 32) && dt != FL_F32)
         M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, m->CTX, H, m->cu, m->work, m->n_work,
-                                       m->hd, scale, m->waves, m->q_prescaled, m->qblocks, s));
+                                       m->hd, scale, m->waves, m->q_prescaled, 2 * m->qblocks, s));
       else if (m->hd == 64)
         M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
                                      (float*)m->CTX, H, m->cu, m->work, m->n_work, scale,
