@@ -103,8 +103,8 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this backend is measured on one GPU; multi-GPU serving is "
-                                   "independent replicas per device (see DESIGN.md), --gpus must "
-                                   "be 1"}))
+                                   "one independent model replica per device with a host-side "
+                                   "split of the sequences, --gpus must be 1"}))
         sys.exit(2)
 
     fl = _package()

@@ -6,7 +6,7 @@
  * (internal/device/cuda_bridge.h:11-53 called from cuda_linux.go) behind the
  * Go `device.Backend` / `device.Tensor` interfaces
  * (internal/device/device.go:5-162).  A Go cgo file binds it the way
- * cuda_linux.go binds cuda_bridge.h (see INTEGRATION.md).
+ * cuda_linux.go binds cuda_bridge.h.
  *
  * Conventions
  *  - Every entry point returns an int status: FL_OK (0) or an FL_ERR_* code;
