@@ -34,6 +34,9 @@
 #ifndef FL_GEMM_W4
 #define FL_GEMM_W4 1
 #endif
+#ifndef FL_GEMM_FUSE
+#define FL_GEMM_FUSE 1
+#endif
 #ifndef FL_GEMM_PP_GROUP_M
 #define FL_GEMM_PP_GROUP_M 8
 #endif
@@ -1194,6 +1197,38 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
 
+  // FUSE: the next tile's first K step (accumulating into 0, no DMA) runs
+  // inside this tile's epilogue, each of its MFMAs right after the four
+  // accumulator reads of the tile it restarts, so the MFMAs execute while the
+  // reads and the epilogue's math issue.  fused_read(t, h, v) returns the
+  // accumulators of row block t, feature group h (v[f] = tile 8(4h+f) + t).
+  constexpr bool FUSE = FL_GEMM_FUSE && EPI != EPI_ROPE;
+  auto fused_read = [&](auto tc, auto hc, float4_t (&v)[4]) __attribute__((always_inline)) {
+    constexpr int TB = decltype(tc)::value, HB = decltype(hc)::value;
+    constexpr uint32_t RD1 = (1 % NS) * STAGE;
+    float x[16];
+#define FL_W4_FUSED_ASM(name)                                                               \
+  asm volatile(name                                                                         \
+               : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), \
+                 "=&v"(x[6]), "=&v"(x[7]), "=&v"(x[8]), "=&v"(x[9]), "=&v"(x[10]),           \
+                 "=&v"(x[11]), "=&v"(x[12]), "=&v"(x[13]), "=&v"(x[14]), "=&v"(x[15])        \
+               : "v"(rdA + RD1), "v"(rdB + RD1)                                            \
+               : "memory", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A)
+#define FL_W4_FUSED_CASE(t, h)                                                              \
+  if constexpr (TB == t && HB == h) {                                                       \
+    if constexpr (F16T) FL_W4_FUSED_ASM(FL_W4_FUSED_F16_##t##_##h);                         \
+    else FL_W4_FUSED_ASM(FL_W4_FUSED_BF16_##t##_##h);                                       \
+  }
+    FL_W4_FUSED_CASE(0, 0) FL_W4_FUSED_CASE(0, 1) FL_W4_FUSED_CASE(1, 0) FL_W4_FUSED_CASE(1, 1)
+    FL_W4_FUSED_CASE(2, 0) FL_W4_FUSED_CASE(2, 1) FL_W4_FUSED_CASE(3, 0) FL_W4_FUSED_CASE(3, 1)
+    FL_W4_FUSED_CASE(4, 0) FL_W4_FUSED_CASE(4, 1) FL_W4_FUSED_CASE(5, 0) FL_W4_FUSED_CASE(5, 1)
+    FL_W4_FUSED_CASE(6, 0) FL_W4_FUSED_CASE(6, 1) FL_W4_FUSED_CASE(7, 0) FL_W4_FUSED_CASE(7, 1)
+#undef FL_W4_FUSED_CASE
+#undef FL_W4_FUSED_ASM
+#pragma unroll
+    for (int f = 0; f < 4; ++f) v[f] = float4_t{x[4 * f], x[4 * f + 1], x[4 * f + 2], x[4 * f + 3]};
+  };
+
   // Epilogue: accumulator tiles come out four at a time (one 16-row block
   // of one 64-feature group), so the compiler's registers stay below v128.
   // Each 16-row block of the wave's outputs (RB bytes per row) is assembled
@@ -1277,8 +1312,15 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       };
       auto block = [&](auto hc) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
-        float4_t v[4] = {W4Acc<(4 * h + 0) * 8 + t>::read(), W4Acc<(4 * h + 1) * 8 + t>::read(),
-                         W4Acc<(4 * h + 2) * 8 + t>::read(), W4Acc<(4 * h + 3) * 8 + t>::read()};
+        float4_t v[4];
+        if constexpr (FUSE && ROT) {
+          fused_read(std::integral_constant<int, t>{}, hc, v);
+        } else {
+          v[0] = W4Acc<(4 * h + 0) * 8 + t>::read();
+          v[1] = W4Acc<(4 * h + 1) * 8 + t>::read();
+          v[2] = W4Acc<(4 * h + 2) * 8 + t>::read();
+          v[3] = W4Acc<(4 * h + 3) * 8 + t>::read();
+        }
         pp_epilogue_block<T, EPI, MATH, HB, ROT>(
             p, v, cbase + h * 64, ln, [&](int f) { return bv[h][f]; },
             [&](int k) { return cs[u % (RD + 1)][k]; }, put);
@@ -1389,7 +1431,9 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   using VM2 = std::conditional_t<PRE3, VME, VM8>;
   const int G4 = nk / 4;
   for (int ti = 0; ti < my_tiles; ++ti) {
-    kstep(I0{}, ZF{}, VM63{});
+    // With FUSE, every tile but the first had its first step in the
+    // previous epilogue.
+    if (!FUSE || ti == 0) kstep(I0{}, ZF{}, VM63{});
     if (ti == 0) {
       kstep(I1{}, Z0{}, VM8{});
       kstep(I2{}, Z0{}, VM8{});
