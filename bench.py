@@ -226,6 +226,14 @@ def main():
         e2e = {"max_seqs": ms_, "max_tokens": mt_, "batches": nb,
                "pipelined_embeddings_per_s": round(len(lengths) / pipe_s, 1),
                "sequential_embeddings_per_s": round(len(lengths) / seq_s, 1)}
+        # The same with one batch per call (a budget as large as the workload;
+        # 288 GB of HBM holds it easily).
+        big = int(lengths.sum())
+        model.embed(ids, lengths, len(lengths), big)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            model.embed(ids, lengths, len(lengths), big)
+        e2e["whole_batch_embeddings_per_s"] = round(len(lengths) * reps / (time.perf_counter() - t0), 1)
         log(f"end to end: {e2e}")
 
     cpu = None
