@@ -189,6 +189,23 @@ int fl_slice(fl_context *ctx, int dtype, const void *src, int rows, int cols, in
 int fl_mean_pool(fl_context *ctx, int dtype, const void *hidden, int cols,
                  const int64_t *lengths, int nseq, int l2, float *out);
 
+/* No counterpart in the reference.  fl_mean_pool for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments and the same results, bit
+ * for bit, but it calls no hipMalloc / hipFree / host-to-device copy.  The
+ * sequence lengths travel in the kernel arguments; cu_seqlens and the partial
+ * sums go to a static scratch array of FL_NOALLOC_PARTIAL_BYTES + 4 KiB that
+ * each GPU the library runs on holds until the process ends.  Limits (else
+ * FL_ERR_INVALID): nseq <= FL_NOALLOC_MAX_SEQS and
+ * nseq * ceil(max(lengths) / 64) * cols * 4 <= FL_NOALLOC_PARTIAL_BYTES.
+ * Every call on one GPU shares that GPU's array: calls of one context are
+ * ordered on its stream, but calls that overlap on one GPU (several contexts
+ * or streams at once) race. */
+#define FL_NOALLOC_MAX_SEQS 512
+#define FL_NOALLOC_PARTIAL_BYTES (16 << 20)
+int fl_mean_pool_noalloc(fl_context *ctx, int dtype, const void *hidden, int cols,
+                         const int64_t *lengths, int nseq, int l2, float *out);
+
 /* ---- Model-level forward (BertModel.ForwardBatch, bert.go:149-169) ----- */
 typedef struct {
   int32_t vocab_size;   /* BertConfig fields (bert.go:20-30) */

@@ -95,6 +95,7 @@ _SIGS = {
     "fl_has_nan": ([_vp, _vp, _i, _i64, C.POINTER(_i)], _i),
     "fl_slice": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp], _i),
     "fl_mean_pool": ([_vp, _i, _vp, _i, _vp, _i, _i, _vp], _i),
+    "fl_mean_pool_noalloc": ([_vp, _i, _vp, _i, _vp, _i, _i, _vp], _i),
     "fl_model_create": ([_vp, C.POINTER(ModelConfigC), C.POINTER(_vp)], _i),
     "fl_model_free": ([_vp], _i),
     "fl_model_set_weight": ([_vp, _cp, _vp, _i64], _i),
@@ -329,11 +330,17 @@ class Context:
                              out.ptr))
         return out
 
-    def mean_pool(self, hidden: DeviceArray, lengths, l2=True) -> DeviceArray:
+    def mean_pool(self, hidden: DeviceArray, lengths, l2=True, out: DeviceArray = None,
+                  noalloc: bool = False) -> DeviceArray:
+        """Masked mean-pool (+L2) of packed rows.  noalloc=True calls
+        fl_mean_pool_noalloc, which allocates nothing on the device (out must
+        then be given)."""
         lengths = np.ascontiguousarray(lengths, np.int64)
-        out = self.empty((lengths.size, hidden.shape[1]), F32)
-        check(lib().fl_mean_pool(self.h, hidden.dtype, hidden.ptr, hidden.shape[1],
-                                 lengths.ctypes.data, lengths.size, int(l2), out.ptr))
+        if out is None:
+            out = self.empty((lengths.size, hidden.shape[1]), F32)
+        f = lib().fl_mean_pool_noalloc if noalloc else lib().fl_mean_pool
+        check(f(self.h, hidden.dtype, hidden.ptr, hidden.shape[1], lengths.ctypes.data,
+                lengths.size, int(l2), out.ptr))
         return out
 
 

@@ -1,6 +1,7 @@
 // api.cpp -- C ABI: context, buffers and per-op entry points
 // (the Tensor methods of internal/device/device.go:5-116 on HIP).
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -177,6 +178,13 @@ int fl_init(int device, fl_context** out) {
     return hip_fail(e, "hipMalloc(flag)");
   }
   ctx->flag = (int*)f;
+  e = noalloc_scratch(device, &ctx->noalloc);
+  if (e != hipSuccess) {
+    (void)hipFree(f);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  }
   *out = ctx;
   return FL_OK;
 }
@@ -236,6 +244,9 @@ int fl_set_device(fl_context* ctx, int device) {
   e = hipMalloc(&f, 256);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(flag)");
   ctx->flag = (int*)f;
+  ctx->noalloc = nullptr;
+  e = noalloc_scratch(device, &ctx->noalloc);
+  if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
   return FL_OK;
 }
 
@@ -757,6 +768,38 @@ int fl_mean_pool(fl_context* ctx, int dtype, const void* hidden, int cols, const
   FL_CHECK_LAUNCH(launch_mean_pool_staged(dtype, hidden, cols, (const int*)ws, nseq, max_len, l2,
                                           (float*)(ws + cu_bytes), out, nullptr, rpc, ctx->stream));
   FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
+  return FL_OK;
+}
+
+int fl_mean_pool_noalloc(fl_context* ctx, int dtype, const void* hidden, int cols,
+                         const int64_t* lengths, int nseq, int l2, float* out) {
+  FL_ENTER(ctx);
+  if (!valid_dtype(dtype) || cols <= 0 || nseq < 0 || (nseq && (!hidden || !lengths || !out)))
+    return fail(FL_ERR_INVALID, "fl_mean_pool_noalloc");
+  if (nseq == 0) return FL_OK;
+  if (nseq > FL_NOALLOC_MAX_SEQS)
+    return fail(FL_ERR_INVALID, "fl_mean_pool_noalloc: more than " +
+                                    std::to_string(FL_NOALLOC_MAX_SEQS) + " sequences");
+  NoAllocLengths la;
+  la.n = nseq;
+  int64_t total = 0;
+  int max_len = 0;
+  for (int b = 0; b < nseq; ++b) {
+    if (lengths[b] <= 0) return fail(FL_ERR_INVALID, "mean pool needs non-empty sequences");
+    total += lengths[b];
+    if (total > INT32_MAX) return fail(FL_ERR_INVALID, "fl_mean_pool_noalloc: too many rows");
+    la.len[b] = (int)lengths[b];
+    max_len = la.len[b] > max_len ? la.len[b] : max_len;
+  }
+  const int64_t chunks = (max_len + kNoAllocRowsPerChunk - 1) / kNoAllocRowsPerChunk;
+  const int64_t need = (int64_t)nseq * chunks * cols * 4;
+  if (need > (int64_t)FL_NOALLOC_PARTIAL_BYTES)
+    return fail(FL_ERR_INVALID, "fl_mean_pool_noalloc: partial sums need " +
+                                    std::to_string(need) + " bytes, the scratch array holds " +
+                                    std::to_string((int64_t)FL_NOALLOC_PARTIAL_BYTES));
+  if (!ctx->noalloc) return fail(FL_ERR_HIP, "fl_mean_pool_noalloc: no scratch address");
+  FL_CHECK_LAUNCH(launch_mean_pool_noalloc(dtype, hidden, cols, la, max_len, l2, out,
+                                           ctx->noalloc, ctx->stream));
   return FL_OK;
 }
 

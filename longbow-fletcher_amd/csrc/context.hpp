@@ -33,6 +33,9 @@ struct fl_context {
   void* ws = nullptr;
   size_t ws_size = 0;
   int* flag = nullptr;  // 4-byte device flag (HasNaN)
+  // The current device's static scratch array of fl_mean_pool_noalloc
+  // (noalloc_scratch), looked up when the context is set to a device.
+  void* noalloc = nullptr;
 
   // RoPE (cos, sin) tables keyed by (base bits, half dim); capacity in positions.
   struct RopeTable {

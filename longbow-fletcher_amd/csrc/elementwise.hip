@@ -3,6 +3,8 @@
 // Add / Scale / AddScalar / AddBias / Gelu / Tanh / Softmax / Cast / HasNaN /
 // Gather / Slice / ApplyRoPE, plus the masked mean-pool (+L2) and CLS gather
 // that turn last hidden states into one vector per sequence.
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -446,6 +448,70 @@ hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, cons
   hipLaunchKernelGGL(pool_final_kernel, dim3(nseq), dim3(256), 0, s, partial, cols, cu_seqlens,
                      rows_per_chunk, max_chunks, l2, out, nan_flag);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free mean pool (fl_mean_pool_noalloc).  Its cu_seqlens and
+// partial sums live in `scratch`, a static array every GPU the library runs on
+// holds until the process ends: cu_seqlens in the first kNoAllocCuBytes, the
+// partial sums after them.  Host code never passes `scratch` itself (in host
+// code the name is a stand-in, not a device address): noalloc_scratch()
+// returns the address of the current device's copy, looked up once per device
+// with hipGetSymbolAddress.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocCuBytes = 4096;
+static_assert((FL_NOALLOC_MAX_SEQS + 1) * 4 <= (int)kNoAllocCuBytes, "cu_seqlens region");
+static __device__ __align__(256) char scratch[kNoAllocCuBytes + FL_NOALLOC_PARTIAL_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+hipError_t noalloc_scratch(int device, void** out) {
+  *out = nullptr;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    // Each GPU holds its own copy of the array at its own address; the
+    // caller has made `device` current.
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != device) return hipErrorInvalidDevice;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+// cu[0] = 0, cu[i + 1] = cu[i] + len[i] (one thread; at most 512 sequences).
+__global__ void cu_from_lengths_kernel(NoAllocLengths a, int* cu) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int s = 0;
+  cu[0] = 0;
+  for (int i = 0; i < a.n; ++i) {
+    s += a.len[i];
+    cu[i + 1] = s;
+  }
+}
+
+hipError_t launch_mean_pool_noalloc(int dtype, const void* hidden, int cols,
+                                    const NoAllocLengths& lengths, int max_len, int l2,
+                                    float* out, void* scratch_dev, hipStream_t s) {
+  if (lengths.n <= 0) return hipSuccess;
+  if (!scratch_dev) return hipErrorInvalidValue;
+  int* cu = (int*)scratch_dev;
+  float* partial = (float*)((char*)scratch_dev + kNoAllocCuBytes);
+  hipLaunchKernelGGL(cu_from_lengths_kernel, dim3(1), dim3(64), 0, s, lengths, cu);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // The same kernels as fl_mean_pool, so the results are identical bit for bit.
+  return launch_mean_pool_staged(dtype, hidden, cols, cu, lengths.n, max_len, l2, partial, out,
+                                 nullptr, kNoAllocRowsPerChunk, s, false);
 }
 
 hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,

@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "../../include/fletcher_hip.h"
+
 namespace fl {
 
 enum EpiKind : int {
@@ -210,6 +212,21 @@ hipError_t launch_mean_pool_staged(int dtype, const void* hidden, int cols, cons
                                    int nseq, int max_len, int l2, float* partial, float* out,
                                    int* nan_flag, int rows_per_chunk, hipStream_t s,
                                    bool tiled = false);
+// fl_mean_pool_noalloc: sequence lengths travel by value in the kernel
+// arguments, cu_seqlens and the partial sums go to the static per-device
+// scratch array (noalloc_scratch); rows_per_chunk is kNoAllocRowsPerChunk, as
+// in fl_mean_pool.
+constexpr int kNoAllocRowsPerChunk = 64;
+struct NoAllocLengths {
+  int n;
+  int len[FL_NOALLOC_MAX_SEQS];
+};
+// Address of the current device's scratch array (`device` must be current);
+// looked up once per device and kept.
+hipError_t noalloc_scratch(int device, void** out);
+hipError_t launch_mean_pool_noalloc(int dtype, const void* hidden, int cols,
+                                    const NoAllocLengths& lengths, int max_len, int l2,
+                                    float* out, void* scratch_dev, hipStream_t s);
 // out[r, c] = silu(in[r, c]) * in[r, inter + c] over an unfused [rows, 2*inter] product.
 hipError_t launch_swiglu(int dtype, const void* in, int rows, int inter, void* out, int math,
                          hipStream_t s);
