@@ -331,11 +331,14 @@ int fl_model_load_safetensors(fl_model* m, const char* path) {
     if (int st = header_entry(s.hf, it->second, ti)) return st;
     const int64_t want = s.rows * s.cols;
     int64_t have = 1;
+    bool overflow = false;
     std::string shp;
     for (int64_t d : ti.shape) {
-      have *= d;
+      overflow |= __builtin_mul_overflow(have, d, &have);
       shp += (shp.empty() ? "" : " ") + std::to_string(d);
     }
+    if (overflow)
+      return fail(FL_ERR_IO, "tensor \"" + s.hf + "\": shape [" + shp + "] overflows 64 bits");
     if (have != want)
       return fail(FL_ERR_INVALID, "tensor \"" + s.hf + "\" size mismatch: expected " + std::to_string(want) +
                                       ", got " + std::to_string(have) + " (shape [" + shp + "])");
@@ -346,7 +349,8 @@ int fl_model_load_safetensors(fl_model* m, const char* path) {
       return fail(FL_ERR_INVALID, "tensor \"" + s.hf + "\" byte size mismatch: expected " + std::to_string(want * 4) +
                                       ", got " + std::to_string(len));
     if (ti.dtype != "F32") return fail(FL_ERR_UNSUPPORTED, "tensor \"" + s.hf + "\" has dtype " + ti.dtype + ", only F32 supported");
-    if (data_start + ti.end > size)
+    // ti.end >= 0 and data_start <= size (header checks), so this cannot overflow.
+    if (ti.end > size - data_start)
       return fail(FL_ERR_IO, "tensor \"" + s.hf + "\": data runs past the end of the file");
     v.resize((size_t)want);
     if (std::fseek(f.f, (long)(data_start + ti.begin), SEEK_SET) != 0 || std::fread(v.data(), 4, v.size(), f.f) != v.size())

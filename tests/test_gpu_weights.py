@@ -8,6 +8,8 @@ written by the `safetensors` library (HF names, [out, in] linear weights), so
 the parser and the transposition are checked against the format's own writer.
 Error cases follow loader.go's: missing file, short raw stream, missing
 tensor, wrong size, F16 data."""
+import json
+import struct
 import sys
 import time
 
@@ -142,6 +144,25 @@ def test_load_errors(ctx, fl, tmp_path):
         with pytest.raises(fl.FletcherError) as e:
             m.load_safetensors(p)
         assert "shape mismatch for transpose" in str(e.value)
+
+        # Crafted headers whose shape product or data offsets overflow 64 bits
+        # are rejected by the checks, not passed through signed overflow.
+        def crafted(entry):
+            hdr = json.dumps({"embeddings.word_embeddings.weight": entry}).encode()
+            p = tmp_path / "crafted.safetensors"
+            p.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 64)
+            return p
+
+        with pytest.raises(fl.FletcherError) as e:
+            m.load_safetensors(crafted({"dtype": "F32", "shape": [1 << 62, 4],
+                                        "data_offsets": [0, 16]}))
+        assert "overflows" in str(e.value)
+        want_bytes = cfg.vocab_size * cfg.hidden * 4
+        top = (1 << 63) - 1
+        with pytest.raises(fl.FletcherError) as e:
+            m.load_safetensors(crafted({"dtype": "F32", "shape": [cfg.vocab_size, cfg.hidden],
+                                        "data_offsets": [top - want_bytes, top]}))
+        assert e.value.code == fl.ERR_IO and "past the end" in str(e.value)
     finally:
         m.close()
 
