@@ -18,9 +18,15 @@
  *    pointer arithmetic on them.  Tensors are 2-D row-major; `ld` arguments are
  *    row strides in elements.
  *  - All work of a context is enqueued in order on the context's HIP stream;
- *    entry points that hand data back to the host synchronise that stream.
+ *    entry points that hand data back to the host synchronise that stream,
+ *    and the others return without waiting for the device.
  *    Entry points lock the context, so several host threads may share it
  *    (concurrent HTTP requests may share one backend, server.go:225-261).
+ *  - fl_linear / fl_gemm keep the packed form of a weight that lies in an
+ *    fl_alloc buffer between calls; every entry point that writes a buffer
+ *    marks it, so the next call packs it again.  A buffer written by other
+ *    means (kernels of the caller on the context stream) must be marked with
+ *    fl_buffer_written.
  *  - Host arrays (ids, lengths, indices) are int64 like Go's `int` on amd64.
  */
 #ifndef FLETCHER_HIP_H
@@ -106,9 +112,25 @@ int fl_get_stream(fl_context *ctx, void **stream);
 /* Cuda_Alloc (cuda_bridge.h:23).  The buffer is zero-filled, as
  * Backend.GetTensor requires (cpu_backend.go:147-156, device_test.go:98-112). */
 int fl_alloc(fl_context *ctx, int64_t bytes, void **out);
-/* Cuda_FreeBuffer (cuda_bridge.h:24). */
+/* Cuda_FreeBuffer (cuda_bridge.h:24); Backend.PutTensor (device.go:146).  The
+ * buffer goes back to the context's cache without waiting for the device
+ * (like the Metal pool, metal_darwin.go:151-274): a later fl_alloc may hand
+ * it out again, and its work is ordered behind the earlier work on the
+ * context stream.  Work on other streams that reads the buffer must finish
+ * before the buffer is freed. */
 int fl_free(fl_context *ctx, void *ptr);
-/* Cuda_CopyToDevice (cuda_bridge.h:25-26); the host buffer may be reused on return. */
+/* The buffer cache's counters, like the Metal pool's metrics
+ * (metal_darwin.go pool hits / misses / size / buffers): stats[0] hits,
+ * [1] misses, [2] cached bytes, [3] cached buffers, [4] bytes of packed
+ * weights kept by fl_linear / fl_gemm, [5] buffers in use. */
+int fl_pool_stats(fl_context *ctx, int64_t *stats);
+/* Returns every cached (free) buffer to the device (synchronises). */
+int fl_pool_trim(fl_context *ctx);
+/* Marks an fl_alloc buffer as written by code outside this library (drops
+ * the packed copies fl_linear / fl_gemm keep of it). */
+int fl_buffer_written(fl_context *ctx, const void *ptr);
+/* Cuda_CopyToDevice (cuda_bridge.h:25-26); the host buffer may be reused on
+ * return (copies up to 64 MiB go through pinned staging without waiting). */
 int fl_copy_to_device(fl_context *ctx, void *dst, const void *src, int64_t bytes);
 /* Cuda_CopyToHost (cuda_bridge.h:27); waits for prior work on the stream. */
 int fl_copy_to_host(fl_context *ctx, void *dst, const void *src, int64_t bytes);
@@ -249,6 +271,13 @@ int fl_model_load_safetensors(fl_model *model, const char *path);
  * writes [nseq x hidden] fp32 to host `out` (synchronises). */
 int fl_model_forward(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
                      float *out);
+/* fl_model_forward with the pooled vectors delivered as out_dtype: FL_F32
+ * (float [nseq x hidden]) or FL_F16 (IEEE half bits, uint16 [nseq x
+ * hidden], converted on the device with round-to-nearest-even): the
+ * fp16 transport of processOutput's Cast(Float16) + ExtractBytes
+ * (embeddings.go:256-286), half the bytes over PCIe. */
+int fl_model_forward_ex(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
+                        int out_dtype, void *out);
 /* Same over right-padded [nseq x max_len] ids with a 0/1 attention mask
  * (1 = token); padding never enters any computation. */
 int fl_model_forward_padded(fl_model *model, const int64_t *ids, const int64_t *mask, int nseq,
@@ -273,6 +302,11 @@ int fl_model_forward_device(fl_model *model, const int32_t *d_ids, const int64_t
 int fl_model_embed(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
                    int max_seqs, int64_t max_tokens, float *out, int32_t *batch_nan,
                    int *nbatches);
+/* fl_model_embed with the pooled vectors delivered as out_dtype (FL_F32 or
+ * FL_F16, as in fl_model_forward_ex). */
+int fl_model_embed_ex(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
+                      int max_seqs, int64_t max_tokens, int out_dtype, void *out,
+                      int32_t *batch_nan, int *nbatches);
 /* Tensor.HasNaN on the pooled output of the previous forward (computed inside
  * the pooling kernel, embeddings.go:757-764) and whether any id was outside
  * [0, vocab) (such ids read row 0).  Synchronises. */

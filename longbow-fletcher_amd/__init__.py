@@ -71,6 +71,9 @@ _SIGS = {
     "fl_get_stream": ([_vp, C.POINTER(_vp)], _i),
     "fl_alloc": ([_vp, _i64, C.POINTER(_vp)], _i),
     "fl_free": ([_vp, _vp], _i),
+    "fl_pool_stats": ([_vp, C.POINTER(_i64)], _i),
+    "fl_pool_trim": ([_vp], _i),
+    "fl_buffer_written": ([_vp, _vp], _i),
     "fl_copy_to_device": ([_vp, _vp, _vp, _i64], _i),
     "fl_copy_to_host": ([_vp, _vp, _vp, _i64], _i),
     "fl_copy_device": ([_vp, _vp, _vp, _i64], _i),
@@ -103,6 +106,8 @@ _SIGS = {
     "fl_model_embed": ([_vp, _vp, _vp, _i, _i, _i64, _vp, _vp, C.POINTER(_i)], _i),
     "fl_model_load_safetensors": ([_vp, _cp], _i),
     "fl_model_forward": ([_vp, _vp, _vp, _i, _vp], _i),
+    "fl_model_forward_ex": ([_vp, _vp, _vp, _i, _i, _vp], _i),
+    "fl_model_embed_ex": ([_vp, _vp, _vp, _i, _i, _i64, _i, _vp, _vp, C.POINTER(_i)], _i),
     "fl_model_forward_padded": ([_vp, _vp, _vp, _i, _i, _vp], _i),
     "fl_model_forward_device": ([_vp, _vp, _vp, _i, _vp], _i),
     "fl_model_status": ([_vp, C.POINTER(_i), C.POINTER(_i)], _i),
@@ -216,6 +221,20 @@ class Context:
         a, t = C.c_int64(), C.c_int64()
         check(lib().fl_vram_usage(self.h, C.byref(a), C.byref(t)))
         return a.value, t.value
+
+    def pool_stats(self) -> dict:
+        """The buffer cache's counters (hits, misses, cached bytes / buffers,
+        packed-weight bytes, buffers in use)."""
+        st = (C.c_int64 * 6)()
+        check(lib().fl_pool_stats(self.h, st))
+        return dict(zip(("hits", "misses", "cached_bytes", "cached_buffers", "packed_bytes",
+                         "live_buffers"), list(st)))
+
+    def pool_trim(self):
+        check(lib().fl_pool_trim(self.h))
+
+    def buffer_written(self, t: "DeviceArray"):
+        check(lib().fl_buffer_written(self.h, t.ptr))
 
     def stream(self) -> int:
         s = C.c_void_p()
@@ -398,26 +417,34 @@ class Model:
         check(lib().fl_model_load_safetensors(self.h, os.fsencode(path)))
         return self
 
-    def forward(self, ids, lengths) -> np.ndarray:
+    def forward(self, ids, lengths, out_dtype: int = F32) -> np.ndarray:
+        """Pooled vectors, float32 or (out_dtype=F16) float16 converted on the
+        device (processOutput's fp16 transport, embeddings.go:256-286)."""
         ids = np.ascontiguousarray(ids, np.int64)
         lengths = np.ascontiguousarray(lengths, np.int64)
-        out = np.zeros((lengths.size, self.cfg.hidden), np.float32)
-        check(lib().fl_model_forward(self.h, ids.ctypes.data, lengths.ctypes.data, lengths.size,
-                                     out.ctypes.data))
+        out = np.zeros((lengths.size, self.cfg.hidden), _NP.get(out_dtype, np.uint16))
+        if out_dtype == F32:
+            check(lib().fl_model_forward(self.h, ids.ctypes.data, lengths.ctypes.data,
+                                         lengths.size, out.ctypes.data))
+        else:
+            check(lib().fl_model_forward_ex(self.h, ids.ctypes.data, lengths.ctypes.data,
+                                            lengths.size, out_dtype, out.ctypes.data))
         return out
 
-    def embed(self, ids, lengths, max_seqs: int = 512, max_tokens: int = 16384):
+    def embed(self, ids, lengths, max_seqs: int = 512, max_tokens: int = 16384,
+              out_dtype: int = F32):
         """All sequences through token-budget batches with overlapped copies
         (runInferenceOnDevice, embeddings.go:690-775).  Returns (pooled
-        [nseq, hidden] fp32, per-sequence NaN flag of its batch, batch count)."""
+        [nseq, hidden] float32 or float16, per-sequence NaN flag of its batch,
+        batch count)."""
         ids = np.ascontiguousarray(ids, np.int64)
         lengths = np.ascontiguousarray(lengths, np.int64)
-        out = np.zeros((lengths.size, self.cfg.hidden), np.float32)
+        out = np.zeros((lengths.size, self.cfg.hidden), _NP.get(out_dtype, np.uint16))
         nan = np.zeros(lengths.size, np.int32)
         nb = C.c_int()
-        check(lib().fl_model_embed(self.h, ids.ctypes.data, lengths.ctypes.data, lengths.size,
-                                   int(max_seqs), int(max_tokens), out.ctypes.data,
-                                   nan.ctypes.data, C.byref(nb)))
+        check(lib().fl_model_embed_ex(self.h, ids.ctypes.data, lengths.ctypes.data, lengths.size,
+                                      int(max_seqs), int(max_tokens), out_dtype, out.ctypes.data,
+                                      nan.ctypes.data, C.byref(nb)))
         return out, nan.astype(bool), nb.value
 
     def forward_padded(self, ids, mask) -> np.ndarray:

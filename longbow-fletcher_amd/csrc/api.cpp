@@ -24,6 +24,10 @@ int fail(int code, const std::string& msg) {
 
 int hip_fail(hipError_t e, const char* what) {
   g_err = std::string(what) + ": " + hipGetErrorString(e);
+  // A failed call also sets the runtime's last error, which the next launch
+  // check (hipGetLastError) would report.  Out-of-memory is recoverable:
+  // clear it so the context keeps working.
+  if (e == hipErrorOutOfMemory) (void)hipGetLastError();
   return e == hipErrorOutOfMemory ? FL_ERR_OOM : FL_ERR_HIP;
 }
 
@@ -42,10 +46,10 @@ int device_alloc(fl_context* ctx, size_t bytes, void** out) {
   return FL_OK;
 }
 
-void device_free(fl_context* ctx, void* p) {
+void device_free(fl_context* ctx, void* p, size_t bytes) {
   if (!p) return;
   (void)hipFree(p);
-  (void)ctx;
+  ctx->allocated -= (int64_t)bytes;
 }
 
 void* workspace(fl_context* ctx, size_t bytes, int* status) {
@@ -100,6 +104,8 @@ const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int
     *status = hip_fail(e, "hipStreamSynchronize");
     return nullptr;
   }
+  // A replaced table stays allocated (and counted) until teardown: a model
+  // keeps the pointer it was handed for its own lengths.
   if (t.cs) ctx->rope_retired.push_back(t.cs);
   t.cs = nullptr;
   t.cap = 0;
@@ -109,6 +115,8 @@ const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int
     *status = hip_fail(e, "hipMalloc(rope)");
     return nullptr;
   }
+  ctx->allocated += (int64_t)(host.size() * sizeof(float2));
+  ctx->rope_bytes += (int64_t)(host.size() * sizeof(float2));
   e = hipMemcpy(p, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     *status = hip_fail(e, "hipMemcpy(rope)");
@@ -138,6 +146,25 @@ using namespace fl;
   } while (0)
 
 static bool valid_dtype(int dt) { return dt == FL_F32 || dt == FL_F16 || dt == FL_BF16; }
+
+// What a PackKey's `kind` packs.
+enum PackKind { PK_GEMM_B = 1, PK_LINEAR_W = 2, PK_LINEAR_BIAS = 3 };
+
+// The packed form of a weight: kept between calls when the source is an
+// fl_alloc buffer (repacked after it is written), else packed into `fallback`
+// (per-call scratch).
+static const void* packed(fl_context* ctx, const fl_context::PackKey& key, size_t bytes,
+                          const std::function<hipError_t(void*)>& pack, void* fallback,
+                          int* st) {
+  const void* p = cached_pack(ctx, key, bytes, pack, st);
+  if (p || *st) return p;
+  hipError_t e = pack(fallback);
+  if (e != hipSuccess) {
+    *st = hip_fail(e, "pack");
+    return nullptr;
+  }
+  return fallback;
+}
 
 extern "C" {
 
@@ -195,8 +222,7 @@ int fl_free_context(fl_context* ctx) {
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (auto& kv : ctx->allocs) (void)hipFree(kv.first);
-    ctx->allocs.clear();
+    release_memory_layer(ctx);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& kv : ctx->rope)
@@ -229,6 +255,8 @@ int fl_set_device(fl_context* ctx, int device) {
     if (kv.second.cs) (void)hipFree(kv.second.cs);
   for (float2* p : ctx->rope_retired) (void)hipFree(p);
   ctx->rope_retired.clear();
+  ctx->allocated -= ctx->rope_bytes;
+  ctx->rope_bytes = 0;
   ctx->ws = nullptr;
   ctx->ws_size = 0;
   ctx->flag = nullptr;
@@ -274,16 +302,18 @@ int fl_get_stream(fl_context* ctx, void** stream) {
 int fl_alloc(fl_context* ctx, int64_t bytes, void** out) {
   FL_ENTER(ctx);
   if (!out || bytes < 0) return fail(FL_ERR_INVALID, "bad allocation request");
+  *out = nullptr;
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, bytes > 0 ? (size_t)bytes : 16);
-  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
-  e = hipMemsetAsync(p, 0, bytes > 0 ? (size_t)bytes : 16, ctx->stream);
+  size_t cls = 0;
+  if (int st = pool_get(ctx, bytes > 0 ? (size_t)bytes : 16, &p, &cls)) return st;
+  // Backend.GetTensor hands out zeroed memory (cpu_backend.go:147-156); the
+  // fill is ordered on the stream after any earlier use of a reused block.
+  hipError_t e = hipMemsetAsync(p, 0, bytes > 0 ? (size_t)bytes : 16, ctx->stream);
   if (e != hipSuccess) {
-    (void)hipFree(p);
+    pool_put(ctx, p, cls, ctx->device);
     return hip_fail(e, "hipMemsetAsync");
   }
-  ctx->allocs[p] = bytes;
-  ctx->allocated += bytes;
+  ctx->live[(uintptr_t)p] = fl_context::Live{cls, ctx->device, ++ctx->gen_counter};
   *out = p;
   return FL_OK;
 }
@@ -291,13 +321,41 @@ int fl_alloc(fl_context* ctx, int64_t bytes, void** out) {
 int fl_free(fl_context* ctx, void* ptr) {
   FL_ENTER(ctx);
   if (!ptr) return FL_OK;
-  auto it = ctx->allocs.find(ptr);
-  if (it == ctx->allocs.end()) return fail(FL_ERR_INVALID, "pointer not allocated by fl_alloc");
-  // Stream-ordered: earlier work on the buffer completes before it is freed.
+  auto it = ctx->live.find((uintptr_t)ptr);
+  if (it == ctx->live.end()) return fail(FL_ERR_INVALID, "pointer not allocated by fl_alloc");
+  // No wait: the block goes back to the cache, and whatever reuses it is
+  // enqueued on the same stream behind the work already using it.
+  drop_packs(ctx, it->first, it->second.cls);
+  pool_put(ctx, ptr, it->second.cls, it->second.device);
+  ctx->live.erase(it);
+  return FL_OK;
+}
+
+int fl_pool_stats(fl_context* ctx, int64_t* stats) {
+  FL_ENTER(ctx);
+  if (!stats) return fail(FL_ERR_INVALID, "null stats");
+  int64_t nbuf = 0;
+  for (auto& kv : ctx->cached) nbuf += (int64_t)kv.second.size();
+  stats[0] = ctx->pool_hits;
+  stats[1] = ctx->pool_misses;
+  stats[2] = ctx->cached_bytes;
+  stats[3] = nbuf;
+  stats[4] = ctx->pack_bytes;
+  stats[5] = (int64_t)ctx->live.size();
+  return FL_OK;
+}
+
+int fl_buffer_written(fl_context* ctx, const void* ptr) {
+  FL_ENTER(ctx);
+  if (!ptr) return fail(FL_ERR_INVALID, "null pointer");
+  note_write(ctx, ptr);
+  return FL_OK;
+}
+
+int fl_pool_trim(fl_context* ctx) {
+  FL_ENTER(ctx);
   FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
-  ctx->allocated -= it->second;
-  ctx->allocs.erase(it);
-  FL_CHECK_LAUNCH(hipFree(ptr));
+  pool_trim(ctx);
   return FL_OK;
 }
 
@@ -305,10 +363,10 @@ int fl_copy_to_device(fl_context* ctx, void* dst, const void* src, int64_t bytes
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
   if (bytes == 0) return FL_OK;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, ctx->stream));
-  // Pageable sources are consumed before return; make that unconditional.
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
-  return FL_OK;
+  note_write(ctx, dst);
+  // The host buffer may be reused on return: small copies go through a
+  // pinned slot without waiting, large ones wait.
+  return stage_upload(ctx, dst, src, (size_t)bytes);
 }
 
 int fl_copy_to_host(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
@@ -324,6 +382,7 @@ int fl_copy_device(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
   if (bytes == 0) return FL_OK;
+  note_write(ctx, dst);
   FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, ctx->stream));
   return FL_OK;
 }
@@ -332,6 +391,7 @@ int fl_memset(fl_context* ctx, void* ptr, int value, int64_t bytes) {
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && !ptr)) return fail(FL_ERR_INVALID, "bad memset");
   if (bytes == 0) return FL_OK;
+  note_write(ctx, ptr);
   FL_CHECK_LAUNCH(hipMemsetAsync(ptr, value, (size_t)bytes, ctx->stream));
   return FL_OK;
 }
@@ -342,20 +402,16 @@ int fl_upload_f32(fl_context* ctx, void* dst, int dtype, const float* src, int64
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!dst || !src)))
     return fail(FL_ERR_INVALID, "bad upload");
   if (n == 0) return FL_OK;
-  if (dtype == FL_F32) {
-    FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
-    FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
-    return FL_OK;
-  }
+  note_write(ctx, dst);
+  if (dtype == FL_F32) return stage_upload(ctx, dst, src, (size_t)n * 4);
   if (rounding == FL_ROUND_TRUNCATE && dtype != FL_F16)
     return fail(FL_ERR_UNSUPPORTED, "truncating upload is defined for fp16 only");
   int st;
   float* tmp = (float*)workspace(ctx, (size_t)n * 4, &st);
   if (st) return st;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(tmp, src, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+  if (int s2 = stage_upload(ctx, tmp, src, (size_t)n * 4)) return s2;
   FL_CHECK_LAUNCH(launch_cast(tmp, FL_F32, dst, dtype, n, rounding == FL_ROUND_TRUNCATE,
                               ctx->stream));
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
 }
 
@@ -387,6 +443,7 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
   if (!valid_dtype(dtype) || m < 0 || n < 0 || k < 0 || !a || !b || !c)
     return fail(FL_ERR_INVALID, "fl_gemm: bad arguments");
   if (m == 0 || n == 0) return FL_OK;
+  note_write(ctx, c);
   GemmEpilogue epi;
   if (!trans_a && alpha == 1.0f) {
     // The ping-pong kernel takes B packed [n x k] in its own row order.
@@ -395,10 +452,15 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
     const bool rows_ok = trans_b && !(((uintptr_t)b | ((size_t)ldb * esz)) & 15);
     if (lay >= 0 && ((!trans_b && ldb == n) || rows_ok)) {
       int st;
-      void* w = workspace(ctx, (size_t)n * k * esz, &st);
+      void* scratch = workspace(ctx, (size_t)n * k * esz, &st);
       if (st) return st;
-      if (trans_b) FL_CHECK_LAUNCH(launch_pack_rows(dtype, b, ldb, n, k, w, lay, ctx->stream));
-      else FL_CHECK_LAUNCH(launch_transpose(dtype, b, k, n, w, lay, ctx->stream));
+      auto pack = [&](void* dst) {
+        return trans_b ? launch_pack_rows(dtype, b, ldb, n, k, dst, lay, ctx->stream)
+                       : launch_transpose(dtype, b, k, n, dst, lay, ctx->stream);
+      };
+      const void* w = packed(ctx, {(uintptr_t)b, PK_GEMM_B, dtype, n, k, lay, trans_b ? ldb : -1},
+                             (size_t)n * k * esz, pack, scratch, &st);
+      if (st) return st;
       GemmEpilogue pe;
       pe.layout = lay;
       if (gemm_nt_supported(dtype, m, n, k, a, lda, w, k, c, ldc, pe)) {
@@ -412,10 +474,12 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
       // B is [k x n]: pack to [n x k] for the MFMA kernel when the shape allows.
       if (gemm_nt_supported(dtype, m, n, k, a, lda, a, k, c, ldc, epi) && ldb == n) {
         int st;
-        void* w = workspace(ctx, (size_t)n * k * dtype_size(dtype), &st);
+        void* scratch = workspace(ctx, (size_t)n * k * dtype_size(dtype), &st);
         if (st) return st;
-        FL_CHECK_LAUNCH(launch_transpose(dtype, b, k, n, w, 0, ctx->stream));
-        bnk = w;
+        auto pack = [&](void* dst) { return launch_transpose(dtype, b, k, n, dst, 0, ctx->stream); };
+        bnk = packed(ctx, {(uintptr_t)b, PK_GEMM_B, dtype, n, k, PACK_PLAIN, -1},
+                     (size_t)n * k * dtype_size(dtype), pack, scratch, &st);
+        if (st) return st;
         ldbn = k;
       } else {
         bnk = nullptr;
@@ -441,6 +505,7 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   if (act < FL_ACT_IDENTITY || act > FL_ACT_SWIGLU) return fail(FL_ERR_INVALID, "bad activation");
   if (act == FL_ACT_SWIGLU && out_cols % 2) return fail(FL_ERR_INVALID, "SwiGLU needs even width");
   if (rows == 0) return FL_OK;
+  note_write(ctx, out);
   const size_t esz = dtype_size(dtype);
   // Scratch layout: [fp32 bias][packed W][unfused product]
   const size_t bias_bytes = bias ? ((size_t)out_cols * 4 + 255) / 256 * 256 : 0;
@@ -470,29 +535,42 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   const int lay = gemm_pp_layout(dtype, out_cols, in_cols, epi.kind, math, bias != nullptr);
   epi.layout = lay >= 0 && w_rows_ok ? lay : PACK_PLAIN;
   const int ldy = fused_swiglu ? out_cols / 2 : out_cols;
-  float* bias32 = nullptr;      // packed order for the MFMA kernels
-  float* bias_plain = nullptr;  // column order for the generic kernel
-  if (bias) {
-    bias32 = (float*)ws;
-    bias_plain = (float*)(ws + bias_bytes);
-    FL_CHECK_LAUNCH(launch_cast(bias, dtype, bias_plain, FL_F32, out_cols, 0, ctx->stream));
-    FL_CHECK_LAUNCH(launch_pack_vec_f32(bias_plain, out_cols, bias32, epi.layout, ctx->stream));
-  }
-  epi.bias = bias32;
   const void* wnk = w;
   void* pk = ws + 2 * bias_bytes;
   bool mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, pk, in_cols, y,
                                 ldy, epi);
-  if (mfma && w_layout == FL_W_IN_OUT) {
-    FL_CHECK_LAUNCH(launch_transpose(dtype, w, in_cols, out_cols, pk, epi.layout, ctx->stream));
-    wnk = pk;
-  } else if (mfma && epi.layout != PACK_PLAIN) {
-    FL_CHECK_LAUNCH(launch_pack_rows(dtype, w, in_cols, out_cols, in_cols, pk, epi.layout,
-                                     ctx->stream));
-    wnk = pk;
+  if (mfma && (w_layout == FL_W_IN_OUT || epi.layout != PACK_PLAIN)) {
+    auto pack_w = [&](void* dst) -> hipError_t {
+      if (w_layout == FL_W_IN_OUT)
+        return launch_transpose(dtype, w, in_cols, out_cols, dst, epi.layout, ctx->stream);
+      return launch_pack_rows(dtype, w, in_cols, out_cols, in_cols, dst, epi.layout, ctx->stream);
+    };
+    wnk = packed(ctx, {(uintptr_t)w, PK_LINEAR_W, dtype, in_cols, out_cols, epi.layout, w_layout},
+                 (size_t)out_cols * in_cols * esz, pack_w, pk, &st);
+    if (st) return st;
   }
   if (mfma) mfma = gemm_nt_supported(dtype, rows, out_cols, in_cols, x, in_cols, wnk, in_cols, y,
                                      ldy, epi);
+  // fp32 bias: in the packed row order for the MFMA kernels, in column order
+  // for the generic kernel.  Both the bias and the packed weight are kept
+  // between calls when they are fl_alloc buffers.
+  const int bias_layout = mfma ? epi.layout : -1;
+  const float* bias32 = nullptr;
+  if (bias) {
+    float* stage = (float*)(ws + bias_bytes);
+    auto pack_bias = [&](void* dst) -> hipError_t {
+      if (bias_layout < 0) return launch_cast(bias, dtype, dst, FL_F32, out_cols, 0, ctx->stream);
+      hipError_t e = launch_cast(bias, dtype, stage, FL_F32, out_cols, 0, ctx->stream);
+      if (e != hipSuccess) return e;
+      return launch_pack_vec_f32(stage, out_cols, (float*)dst, bias_layout, ctx->stream);
+    };
+    bias32 = (const float*)packed(
+        ctx, {(uintptr_t)bias, PK_LINEAR_BIAS, dtype, 1, out_cols, bias_layout, 0},
+        (size_t)out_cols * 4, pack_bias, ws, &st);
+    if (st) return st;
+  }
+  epi.bias = mfma ? bias32 : nullptr;
+  const float* bias_plain = mfma ? nullptr : bias32;
   if (mfma) {
     FL_CHECK_LAUNCH(launch_gemm_nt(dtype, x, in_cols, wnk, in_cols, y, ldy, rows, out_cols,
                                    in_cols, epi, ctx->stream));
@@ -517,6 +595,7 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
 int fl_add(fl_context* ctx, int dtype, void* t, const void* other, int64_t n) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!t || !other))) return fail(FL_ERR_INVALID, "fl_add");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_add(dtype, t, other, n, ctx->stream));
   return FL_OK;
 }
@@ -524,6 +603,7 @@ int fl_add(fl_context* ctx, int dtype, void* t, const void* other, int64_t n) {
 int fl_add_scalar(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_add_scalar");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_affine(dtype, t, n, 1.0f, v, ctx->stream));
   return FL_OK;
 }
@@ -532,6 +612,7 @@ int fl_scale(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_scale");
   if (v == 1.0f) return FL_OK;
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_affine(dtype, t, n, v, 0.0f, ctx->stream));
   return FL_OK;
 }
@@ -540,6 +621,7 @@ int fl_add_bias(fl_context* ctx, int dtype, void* t, int rows, int cols, const v
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !bias)
     return fail(FL_ERR_INVALID, "fl_add_bias");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_add_bias(dtype, t, rows, cols, bias, ctx->stream));
   return FL_OK;
 }
@@ -549,6 +631,7 @@ int fl_activation(fl_context* ctx, int dtype, void* t, int rows, int cols, int a
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t) return fail(FL_ERR_INVALID, "fl_activation");
   if (act != FL_ACT_GELU && act != FL_ACT_TANH && act != FL_ACT_SOFTMAX && act != FL_ACT_IDENTITY)
     return fail(FL_ERR_INVALID, "fl_activation: unsupported activation");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_activation(dtype, t, rows, cols, act, math, ctx->stream));
   return FL_OK;
 }
@@ -559,6 +642,7 @@ int fl_layernorm(fl_context* ctx, int dtype, void* t, int rows, int cols, const 
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !gamma || !beta)
     return fail(FL_ERR_INVALID, "fl_layernorm");
   if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_layernorm: cols > 4096");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_layernorm(dtype, t, nullptr, rows, cols, gamma, beta, eps, ctx->stream));
   return FL_OK;
 }
@@ -569,6 +653,7 @@ int fl_add_layernorm(fl_context* ctx, int dtype, void* t, const void* residual, 
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !residual || !gamma || !beta)
     return fail(FL_ERR_INVALID, "fl_add_layernorm");
   if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_add_layernorm: cols > 4096");
+  note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_layernorm(dtype, t, residual, rows, cols, gamma, beta, eps, ctx->stream));
   return FL_OK;
 }
@@ -588,9 +673,9 @@ int fl_gather_rows(fl_context* ctx, int dtype, const void* table, int rows, int 
   int st;
   int* d = (int*)workspace(ctx, (size_t)n * 4, &st);
   if (st) return st;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(d, i32.data(), (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+  note_write(ctx, out);
+  if ((st = stage_upload(ctx, d, i32.data(), (size_t)n * 4))) return st;
   FL_CHECK_LAUNCH(launch_gather(dtype, table, cols, d, n, out, ctx->stream));
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
 }
 
@@ -606,9 +691,9 @@ static int rope_common(fl_context* ctx, int dtype, void* t, const std::vector<in
   if (st) return st;
   int* d = (int*)workspace(ctx, (size_t)rows * 4, &st);
   if (st) return st;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(d, pos.data(), (size_t)rows * 4, hipMemcpyHostToDevice, ctx->stream));
+  note_write(ctx, t);
+  if ((st = stage_upload(ctx, d, pos.data(), (size_t)rows * 4))) return st;
   FL_CHECK_LAUNCH(launch_rope(dtype, t, rows, heads, head_dim, heads * head_dim, d, cs, ctx->stream));
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
 }
 
@@ -673,10 +758,12 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
   int st;
   char* ws = (char*)workspace(ctx, cu_bytes + work.size() * sizeof(AttnWork), &st);
   if (st) return st;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(ws, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
-  if (!work.empty())
-    FL_CHECK_LAUNCH(hipMemcpyAsync(ws + cu_bytes, work.data(), work.size() * sizeof(AttnWork),
-                                   hipMemcpyHostToDevice, ctx->stream));
+  note_write(ctx, out);
+  // cu_seqlens then the work list, one staged copy.
+  std::vector<char> meta(cu_bytes + work.size() * sizeof(AttnWork));
+  std::memcpy(meta.data(), cu.data(), (size_t)(nseq + 1) * 4);
+  if (!work.empty()) std::memcpy(meta.data() + cu_bytes, work.data(), work.size() * sizeof(AttnWork));
+  if ((st = stage_upload(ctx, ws, meta.data(), meta.size()))) return st;
   const int* dcu = (const int*)ws;
   const AttnWork* dwork = (const AttnWork*)(ws + cu_bytes);
   if (fast16) {
@@ -691,7 +778,6 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
     FL_CHECK_LAUNCH(launch_attention_generic(dtype, q, k, v, hidden, out, hidden, dcu, nseq,
                                              max_len, heads, hd, scale, math, ctx->stream));
   }
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
 }
 
@@ -718,6 +804,7 @@ int fl_cast(fl_context* ctx, const void* src, int src_dtype, void* dst, int dst_
   FL_ENTER(ctx);
   if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype) || n < 0 || (n > 0 && (!src || !dst)))
     return fail(FL_ERR_INVALID, "fl_cast");
+  note_write(ctx, dst);
   FL_CHECK_LAUNCH(launch_cast(src, src_dtype, dst, dst_dtype, n, 0, ctx->stream));
   return FL_OK;
 }
@@ -741,6 +828,7 @@ int fl_slice(fl_context* ctx, int dtype, const void* src, int rows, int cols, in
   if (!valid_dtype(dtype) || !src || !dst || r0 < 0 || c0 < 0 || r1 > rows || c1 > cols ||
       r1 - r0 <= 0 || c1 - c0 <= 0)
     return fail(FL_ERR_INVALID, "Slice: invalid dimensions");
+  note_write(ctx, dst);
   FL_CHECK_LAUNCH(launch_slice(dtype, src, cols, r0, r1, c0, c1, dst, ctx->stream));
   return FL_OK;
 }
@@ -764,10 +852,10 @@ int fl_mean_pool(fl_context* ctx, int dtype, const void* hidden, int cols, const
   int st;
   char* ws = (char*)workspace(ctx, cu_bytes + (size_t)nseq * chunks * cols * 4, &st);
   if (st) return st;
-  FL_CHECK_LAUNCH(hipMemcpyAsync(ws, cu.data(), (nseq + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+  note_write(ctx, out);
+  if ((st = stage_upload(ctx, ws, cu.data(), (size_t)(nseq + 1) * 4))) return st;
   FL_CHECK_LAUNCH(launch_mean_pool_staged(dtype, hidden, cols, (const int*)ws, nseq, max_len, l2,
                                           (float*)(ws + cu_bytes), out, nullptr, rpc, ctx->stream));
-  FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
 }
 
@@ -798,6 +886,7 @@ int fl_mean_pool_noalloc(fl_context* ctx, int dtype, const void* hidden, int col
                                     std::to_string(need) + " bytes, the scratch array holds " +
                                     std::to_string((int64_t)FL_NOALLOC_PARTIAL_BYTES));
   if (!ctx->noalloc) return fail(FL_ERR_HIP, "fl_mean_pool_noalloc: no scratch address");
+  note_write(ctx, out);
   FL_CHECK_LAUNCH(launch_mean_pool_noalloc(dtype, hidden, cols, la, max_len, l2, out,
                                            ctx->noalloc, ctx->stream));
   return FL_OK;

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <tuple>
 #include <mutex>
@@ -26,8 +27,52 @@ struct fl_context {
   int device = 0;
   hipStream_t stream = nullptr;
   std::recursive_mutex mu;
-  std::unordered_map<void*, int64_t> allocs;  // buffers handed out by fl_alloc
+  // Device bytes this context holds (fl_vram_usage): pool blocks in use and
+  // cached, workspace, tables, model buffers.
   int64_t allocated = 0;
+
+  // fl_alloc buffers in use, by base address: size class, device, and the
+  // write generation (bumped by every entry point that writes into it).
+  struct Live {
+    size_t cls = 0;
+    int device = 0;
+    uint64_t gen = 0;
+  };
+  std::map<uintptr_t, Live> live;
+  uint64_t gen_counter = 0;
+  // Free blocks by (device, size class), reused in stream order.
+  std::map<std::pair<int, size_t>, std::vector<void*>> cached;
+  int64_t cached_bytes = 0;
+  int64_t pool_hits = 0, pool_misses = 0;
+
+  // Packed weights of fl_linear / fl_gemm, keyed by the source pointer and
+  // how it was packed; valid while the source buffer's generation matches.
+  struct PackKey {
+    uintptr_t src;
+    int kind, dtype, rows, cols, layout, extra;
+    bool operator<(const PackKey& o) const {
+      return std::tie(src, kind, dtype, rows, cols, layout, extra) <
+             std::tie(o.src, o.kind, o.dtype, o.rows, o.cols, o.layout, o.extra);
+    }
+  };
+  struct PackEntry {
+    void* buf = nullptr;
+    size_t cls = 0;
+    uint64_t gen = 0;
+    int device = 0;
+  };
+  std::map<PackKey, PackEntry> packs;
+  int64_t pack_bytes = 0;
+
+  // Pinned host slots of stage_upload, used in turn.
+  static constexpr int kStages = 4;
+  struct Stage {
+    void* host = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+  } stage[kStages];
+  int stage_next = 0;
 
   // Grow-only scratch for per-op temporaries (stream-ordered reuse).
   void* ws = nullptr;
@@ -47,6 +92,7 @@ struct fl_context {
   // Tables replaced by larger ones stay allocated until teardown: a model
   // keeps the pointer it was handed for its own lengths.
   std::vector<float2*> rope_retired;
+  int64_t rope_bytes = 0;  // all tables, current and retired (part of `allocated`)
 };
 
 namespace fl {
@@ -66,7 +112,36 @@ void* workspace(fl_context* ctx, size_t bytes, int* status);
 // p < max_pos: angles and products in float64, cast to float32 once.
 const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status,
                          float scale = 1.0f);
+// hipMalloc / hipFree counted in ctx->allocated (fl_vram_usage).
 int device_alloc(fl_context* ctx, size_t bytes, void** out);
-void device_free(fl_context* ctx, void* p);
+void device_free(fl_context* ctx, void* p, size_t bytes);
+
+// ---- pool.cpp: caching allocator, write tracking, packed weights, staging ----
+constexpr int64_t kPackCacheLimit = (int64_t)8 << 30;  // packed weights kept at most
+constexpr size_t kStageMax = (size_t)64 << 20;          // larger uploads are synchronous
+size_t pool_class(size_t bytes);
+// A block of at least `bytes` on the current device (not zeroed): a cached
+// one when available, else hipMalloc (after giving cached blocks back if the
+// device is full).
+int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls);
+void pool_put(fl_context* ctx, void* p, size_t cls, int device);
+// hipFree of every cached block.
+void pool_trim(fl_context* ctx);
+// The fl_alloc buffer containing ptr, or null.
+fl_context::Live* find_live(fl_context* ctx, const void* ptr);
+// Marks the fl_alloc buffer containing ptr (if any) as written.
+void note_write(fl_context* ctx, const void* ptr);
+// Releases the packed copies of sources inside [base, base + cls).
+void drop_packs(fl_context* ctx, uintptr_t base, size_t cls);
+// The packed form of key.src (an fl_alloc buffer), made by pack(dst) when
+// missing or when the source was written since; null when the source is not
+// an fl_alloc buffer or the cache is full (the caller packs into scratch).
+const void* cached_pack(fl_context* ctx, const fl_context::PackKey& key, size_t bytes,
+                        const std::function<hipError_t(void*)>& pack, int* status);
+// Host -> device copy on the context stream that returns without waiting:
+// the bytes go through a pinned slot (copies over kStageMax are synchronous).
+int stage_upload(fl_context* ctx, void* dst, const void* src, size_t bytes);
+// Frees every pool block, packed weight and staging slot (teardown).
+void release_memory_layer(fl_context* ctx);
 
 }  // namespace fl

@@ -18,6 +18,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "context.hpp"
@@ -69,7 +70,7 @@ struct fl_model {
   std::vector<LayerW> layers;
   float* pool_w = nullptr;  // fp32 [H, H] reference layout
   float* pool_b = nullptr;
-  std::vector<void*> owned;
+  std::unordered_map<void*, size_t> owned;  // device buffers and their sizes
 
   // activations (capacity in tokens / sequences)
   int64_t cap_tokens = 0;
@@ -88,6 +89,7 @@ struct fl_model {
   float* part = nullptr;
   float* cls = nullptr;
   float* out = nullptr;
+  uint16_t* out16 = nullptr;  // fp16 copy of `out` (FL_F16 output)
   int* flags = nullptr;  // [0] NaN in pooled output, [1] id out of range
 
   // Pinned host staging of the per-batch metadata (attention work list,
@@ -111,6 +113,7 @@ struct fl_model {
     int* flags_pin[2] = {nullptr, nullptr};
     int* ids_dev[2] = {nullptr, nullptr};
     float* out_dev[2] = {nullptr, nullptr};
+    uint16_t* out16_dev[2] = {nullptr, nullptr};  // fp16 output of the batch (FL_F16)
     int* flags_dev[2] = {nullptr, nullptr};
     hipEvent_t h2d[2] = {nullptr, nullptr}, fwd[2] = {nullptr, nullptr}, d2h[2] = {nullptr, nullptr};
     int64_t cap_tok = 0;
@@ -146,18 +149,37 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Attention scale 1/float32(sqrt(d)) (bert.go:643).
 float attn_scale(int hd) { return 1.0f / (float)std::sqrt((double)hd); }
 
-int track_alloc(fl_model* m, size_t bytes, void** out) {
-  int st = device_alloc(m->ctx, bytes, out);
+// A model-owned device buffer: counted in the context's allocated bytes and
+// freed with the model.
+template <typename P>
+int track_alloc(fl_model* m, size_t bytes, P*& out) {
+  void* p = nullptr;
+  out = nullptr;
+  int st = device_alloc(m->ctx, bytes, &p);
   if (st) return st;
-  m->owned.push_back(*out);
+  m->owned[p] = bytes;
+  out = (P*)p;
   return FL_OK;
 }
 
-void untrack_free(fl_model* m, void* p) {
+// Frees a buffer from track_alloc and clears the pointer, so that a failed
+// reallocation never leaves a freed buffer in use.
+template <typename P>
+void untrack_free(fl_model* m, P*& p) {
   if (!p) return;
-  auto it = std::find(m->owned.begin(), m->owned.end(), p);
-  if (it != m->owned.end()) m->owned.erase(it);
-  (void)hipFree(p);
+  auto it = m->owned.find((void*)p);
+  size_t bytes = 0;
+  if (it != m->owned.end()) {
+    bytes = it->second;
+    m->owned.erase(it);
+  }
+  device_free(m->ctx, (void*)p, bytes);
+  p = nullptr;
+}
+
+void free_owned(fl_model* m) {
+  for (auto& kv : m->owned) device_free(m->ctx, kv.first, kv.second);
+  m->owned.clear();
 }
 
 #define M_CHECK(expr)                                  \
@@ -223,57 +245,61 @@ bool mfma_shape_ok(int dtype, int N, int K) {
   return gemm_nt_supported(dtype, 1, N, K, dummy, K, dummy, K, dummy, N, e);
 }
 
+// Grows the activation buffers.  Capacities drop to 0 and old buffers are
+// freed (pointers cleared) before anything is allocated, so an allocation
+// that fails leaves a model whose next call reallocates from scratch.
 int ensure_capacity(fl_model* m, int64_t T, int nseq, size_t nwork, size_t part_elems) {
   if (T > m->cap_tokens) {
     M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    for (void* p : {m->X, m->QKV, m->CTX, m->TMP, m->G2, (void*)m->ids32, (void*)m->pos32})
-      untrack_free(m, p);
-    m->G2 = nullptr;
+    m->cap_tokens = 0;
+    m->last_lengths.clear();
+    untrack_free(m, m->X);
+    untrack_free(m, m->QKV);
+    untrack_free(m, m->CTX);
+    untrack_free(m, m->TMP);
+    untrack_free(m, m->G2);
+    untrack_free(m, m->ids32);
+    untrack_free(m, m->pos32);
     // Rows rounded up to whole 256-row tiles (tiled activations, padded GEMM outputs).
     int64_t cap = (std::max<int64_t>(T, 256) + 255) / 256 * 256;
     const int64_t wide = std::max<int64_t>(3 * m->H, m->Ni);
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->X));
-    M_ST(track_alloc(m, (size_t)cap * wide * m->esz, &m->QKV));
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->CTX));
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, &m->TMP));
-    if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, &m->G2));
-    void* p;
-    M_ST(track_alloc(m, (size_t)cap * 4, &p));
-    m->ids32 = (int*)p;
-    M_ST(track_alloc(m, (size_t)cap * 4, &p));
-    m->pos32 = (int*)p;
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->X));
+    M_ST(track_alloc(m, (size_t)cap * wide * m->esz, m->QKV));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->CTX));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->TMP));
+    if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, m->G2));
+    M_ST(track_alloc(m, (size_t)cap * 4, m->ids32));
+    M_ST(track_alloc(m, (size_t)cap * 4, m->pos32));
     m->cap_tokens = cap;
-    m->last_lengths.clear();
   }
   if (nseq > m->cap_seq) {
     M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    for (void* p : {(void*)m->cu, (void*)m->cls, (void*)m->out}) untrack_free(m, p);
-    const int cap = std::max(nseq, 64);
-    void* p;
-    M_ST(track_alloc(m, (size_t)(cap + 1) * 4, &p));
-    m->cu = (int*)p;
-    M_ST(track_alloc(m, (size_t)cap * m->H * 4, &p));
-    m->cls = (float*)p;
-    M_ST(track_alloc(m, (size_t)cap * m->H * 4, &p));
-    m->out = (float*)p;
-    m->cap_seq = cap;
+    m->cap_seq = 0;
     m->last_lengths.clear();
+    untrack_free(m, m->cu);
+    untrack_free(m, m->cls);
+    untrack_free(m, m->out);
+    untrack_free(m, m->out16);
+    const int cap = std::max(nseq, 64);
+    M_ST(track_alloc(m, (size_t)(cap + 1) * 4, m->cu));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, m->cls));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, m->out));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 2, m->out16));
+    m->cap_seq = cap;
   }
   if (nwork > m->cap_work) {
     M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    untrack_free(m, m->work);
-    void* p;
-    M_ST(track_alloc(m, nwork * sizeof(AttnWork), &p));
-    m->work = (AttnWork*)p;
-    m->cap_work = nwork;
+    m->cap_work = 0;
     m->last_lengths.clear();
+    untrack_free(m, m->work);
+    M_ST(track_alloc(m, nwork * sizeof(AttnWork), m->work));
+    m->cap_work = nwork;
   }
   if (part_elems > m->cap_part) {
     M_CHECK(hipStreamSynchronize(m->ctx->stream));
+    m->cap_part = 0;
     untrack_free(m, m->part);
-    void* p;
-    M_ST(track_alloc(m, part_elems * 4, &p));
-    m->part = (float*)p;
+    M_ST(track_alloc(m, part_elems * 4, m->part));
     m->cap_part = part_elems;
   }
   return FL_OK;
@@ -585,15 +611,13 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
   }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
-    void* p;
-    M_ST(track_alloc(m, n * 4, &p));
+    M_ST(track_alloc(m, n * 4, *dst));
     std::vector<float> h(n, v);
-    M_CHECK(hipMemcpy(p, h.data(), n * 4, hipMemcpyHostToDevice));
-    *dst = (float*)p;
+    M_CHECK(hipMemcpy(*dst, h.data(), n * 4, hipMemcpyHostToDevice));
     return FL_OK;
   };
   auto zeros = [&](void** dst, size_t bytes) -> int {
-    M_ST(track_alloc(m, bytes, dst));
+    M_ST(track_alloc(m, bytes, *dst));
     M_CHECK(hipMemset(*dst, 0, bytes));
     return FL_OK;
   };
@@ -622,7 +646,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     m->flags = (int*)f;
   } while (0);
   if (st) {
-    for (void* p : m->owned) (void)hipFree(p);
+    free_owned(m);
     delete m;
     return st;
   }
@@ -647,7 +671,7 @@ int fl_model_free(fl_model* m) {
     }
     for (hipStream_t st : {P.up, P.down})
       if (st) (void)hipStreamDestroy(st);
-    for (void* p : m->owned) (void)hipFree(p);
+    free_owned(m);
     for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
   }
   delete m;
@@ -749,8 +773,13 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
   return FL_OK;
 }
 
+// The pooled output leaves the device as fp32 or, for FL_F16, converted on
+// the device with round-to-nearest-even (processOutput's Cast(Float16) and
+// ExtractBytes, embeddings.go:256-286), half the bytes over PCIe.
+static bool valid_out_dtype(int dt) { return dt == FL_F32 || dt == FL_F16; }
+
 static int forward_common(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
-                          float* out) {
+                          int out_dtype, void* out) {
   if (nseq <= 0) return FL_OK;
   M_ST(prepare(m, lengths, nseq));
   const int64_t T = m->T;
@@ -764,18 +793,30 @@ static int forward_common(fl_model* m, const int64_t* ids, const int64_t* length
   hipStream_t s = m->ctx->stream;
   M_CHECK(hipMemcpyAsync(m->ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
   M_ST(run(m, m->ids32, nseq, m->out, m->flags));
-  M_CHECK(hipMemcpyAsync(out, m->out, (size_t)nseq * m->H * 4, hipMemcpyDeviceToHost, s));
+  const size_t n = (size_t)nseq * m->H;
+  if (out_dtype == FL_F16) {
+    M_CHECK(launch_cast(m->out, FL_F32, m->out16, FL_F16, (int64_t)n, 0, s));
+    M_CHECK(hipMemcpyAsync(out, m->out16, n * 2, hipMemcpyDeviceToHost, s));
+  } else {
+    M_CHECK(hipMemcpyAsync(out, m->out, n * 4, hipMemcpyDeviceToHost, s));
+  }
   M_CHECK(hipStreamSynchronize(s));
   return FL_OK;
 }
 
-int fl_model_forward(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
-                     float* out) {
+int fl_model_forward_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
+                        int out_dtype, void* out) {
   if (!m || (nseq > 0 && (!ids || !lengths || !out))) return fail(FL_ERR_INVALID, "null argument");
   if (nseq < 0) return fail(FL_ERR_INVALID, "negative batch");
+  if (!valid_out_dtype(out_dtype)) return fail(FL_ERR_INVALID, "output dtype must be F32 or F16");
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
-  return forward_common(m, ids, lengths, nseq, out);
+  return forward_common(m, ids, lengths, nseq, out_dtype, out);
+}
+
+int fl_model_forward(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
+                     float* out) {
+  return fl_model_forward_ex(m, ids, lengths, nseq, FL_F32, out);
 }
 
 int fl_model_forward_padded(fl_model* m, const int64_t* ids, const int64_t* mask, int nseq,
@@ -802,7 +843,7 @@ int fl_model_forward_padded(fl_model* m, const int64_t* ids, const int64_t* mask
     if (L == 0) return fail(FL_ERR_INVALID, "sequence with no tokens");
     lengths[b] = L;
   }
-  return forward_common(m, packed.data(), lengths.data(), nseq, out);
+  return forward_common(m, packed.data(), lengths.data(), nseq, FL_F32, out);
 }
 
 int fl_model_forward_device(fl_model* m, const int32_t* d_ids, const int64_t* lengths, int nseq,
@@ -814,13 +855,22 @@ int fl_model_forward_device(fl_model* m, const int32_t* d_ids, const int64_t* le
   M_ST(activate(m->ctx));
   if (nseq == 0) return FL_OK;
   M_ST(prepare(m, lengths, nseq));
+  note_write(m->ctx, d_out);
   return run(m, d_ids, nseq, d_out, m->flags);
 }
 
 int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq, int max_seqs,
                    int64_t max_tokens, float* out, int32_t* batch_nan, int* nbatches) {
+  return fl_model_embed_ex(m, ids, lengths, nseq, max_seqs, max_tokens, FL_F32, out, batch_nan,
+                           nbatches);
+}
+
+int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
+                      int max_seqs, int64_t max_tokens, int out_dtype, void* out,
+                      int32_t* batch_nan, int* nbatches) {
   if (!m || (nseq > 0 && (!ids || !lengths || !out))) return fail(FL_ERR_INVALID, "null argument");
   if (nseq < 0) return fail(FL_ERR_INVALID, "negative batch");
+  if (!valid_out_dtype(out_dtype)) return fail(FL_ERR_INVALID, "output dtype must be F32 or F16");
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
   if (nbatches) *nbatches = 0;
@@ -877,20 +927,23 @@ int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int 
       P.ids_pin[k] = nullptr;
       P.out_pin[k] = nullptr;
       P.flags_pin[k] = nullptr;
-      for (void* d : {(void*)P.ids_dev[k], (void*)P.out_dev[k], (void*)P.flags_dev[k]}) untrack_free(m, d);
+      untrack_free(m, P.ids_dev[k]);
+      untrack_free(m, P.out_dev[k]);
+      untrack_free(m, P.out16_dev[k]);
+      untrack_free(m, P.flags_dev[k]);
+    }
+    // Capacities stay 0 until every buffer of both slots exists: a failure
+    // here leaves null pointers and the next call reallocates.
+    P.cap_tok = P.cap_seq = 0;
+    for (int k = 0; k < 2; ++k) {
       if (hipHostMalloc((void**)&P.ids_pin[k], (size_t)ct * 4, hipHostMallocDefault) != hipSuccess ||
           hipHostMalloc((void**)&P.out_pin[k], (size_t)cq * m->H * 4, hipHostMallocDefault) != hipSuccess ||
-          hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess) {
-        P.cap_tok = P.cap_seq = 0;
+          hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess)
         return fail(FL_ERR_OOM, "hipHostMalloc(embed pipeline)");
-      }
-      void* d;
-      M_ST(track_alloc(m, (size_t)ct * 4, &d));
-      P.ids_dev[k] = (int*)d;
-      M_ST(track_alloc(m, (size_t)cq * m->H * 4, &d));
-      P.out_dev[k] = (float*)d;
-      M_ST(track_alloc(m, 8, &d));
-      P.flags_dev[k] = (int*)d;
+      M_ST(track_alloc(m, (size_t)ct * 4, P.ids_dev[k]));
+      M_ST(track_alloc(m, (size_t)cq * m->H * 4, P.out_dev[k]));
+      M_ST(track_alloc(m, (size_t)cq * m->H * 2, P.out16_dev[k]));
+      M_ST(track_alloc(m, 8, P.flags_dev[k]));
     }
     P.cap_tok = ct;
     P.cap_seq = cq;
@@ -902,11 +955,12 @@ int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int 
   // up to two batches ahead of the device, like the reference's double
   // buffering of outputs (embeddings.go:766-775).
   const int64_t H = m->H;
+  const size_t osz = out_dtype == FL_F16 ? 2 : 4;
   auto drain = [&](int b) -> int {
     const Batch& pb = plan[(size_t)b];
     const int k = b & 1;
     M_CHECK(hipEventSynchronize(P.d2h[k]));
-    std::memcpy(out + (size_t)pb.first * H, P.out_pin[k], (size_t)pb.count * H * 4);
+    std::memcpy((char*)out + (size_t)pb.first * H * osz, P.out_pin[k], (size_t)pb.count * H * osz);
     if (batch_nan)
       for (int i = 0; i < pb.count; ++i) batch_nan[pb.first + i] = P.flags_pin[k][0] != 0;
     return FL_OK;
@@ -922,9 +976,14 @@ int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int 
     M_CHECK(hipStreamWaitEvent(cs, P.h2d[k], 0));
     M_ST(prepare(m, lengths + pb.first, pb.count));
     M_ST(run(m, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
+    const void* dev_out = P.out_dev[k];
+    if (out_dtype == FL_F16) {
+      M_CHECK(launch_cast(P.out_dev[k], FL_F32, P.out16_dev[k], FL_F16, (int64_t)pb.count * H, 0, cs));
+      dev_out = P.out16_dev[k];
+    }
     M_CHECK(hipEventRecord(P.fwd[k], cs));
     M_CHECK(hipStreamWaitEvent(P.down, P.fwd[k], 0));
-    M_CHECK(hipMemcpyAsync(P.out_pin[k], P.out_dev[k], (size_t)pb.count * H * 4, hipMemcpyDeviceToHost, P.down));
+    M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)pb.count * H * osz, hipMemcpyDeviceToHost, P.down));
     M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, P.down));
     M_CHECK(hipEventRecord(P.d2h[k], P.down));
   }

@@ -322,6 +322,45 @@ typedef struct {
   float scale;
 } attn_job;
 
+/* Rows [r0, r1) of an s x s score matrix through the row softmax. */
+typedef struct {
+  float *scores;
+  int s, r0, r1, math_mode;
+} softmax_job;
+
+static void *softmax_rows_worker(void *arg) {
+  softmax_job *j = (softmax_job *)arg;
+  for (int r = j->r0; r < j->r1; r++) {
+    if (j->math_mode == ORC_MATH_EXACT) softmax_exact(j->scores + (int64_t)r * j->s, j->s);
+    else orc_softmax_fast(j->scores + (int64_t)r * j->s, j->s);
+  }
+  return NULL;
+}
+
+/* Every row of the score matrix; rows are independent, so splitting them
+ * over threads (when the caller is the only attention worker) leaves each
+ * row's result unchanged. */
+static void softmax_rows(float *scores, int s, int math_mode, int threads) {
+  if (threads > 64) threads = 64;
+  if (threads <= 1 || s < 256) {
+    softmax_job one = {scores, s, 0, s, math_mode};
+    softmax_rows_worker(&one);
+    return;
+  }
+  pthread_t th[64];
+  softmax_job jobs[64];
+  int per = (s + threads - 1) / threads, n = 0;
+  for (int t = 0; t < threads; t++) {
+    int r0 = t * per, r1 = r0 + per < s ? r0 + per : s;
+    if (r0 >= r1) break;
+    softmax_job jb = {scores, s, r0, r1, math_mode};
+    jobs[n] = jb;
+    pthread_create(&th[n], NULL, softmax_rows_worker, &jobs[n]);
+    n++;
+  }
+  for (int t = 0; t < n; t++) pthread_join(th[t], NULL);
+}
+
 /* Body of one worker of cpu_backend.go:695-753: for each batch item and
  * head, scores = scale * Q_h K_h^T (sgemm, alpha = scale), SoftmaxFast per
  * row, out_h = scores V_h (sgemm into the head's column slice). */
@@ -336,10 +375,7 @@ static void *attn_worker(void *arg) {
       int64_t off = q_start + (int64_t)h * hd;
       orc_sgemm(0, 1, s, s, hd, j->scale, j->q + off, c, j->k + off, c, 0.0f,
                 scores, s);
-      for (int r = 0; r < s; r++) {
-        if (j->math_mode == ORC_MATH_EXACT) softmax_exact(scores + (int64_t)r * s, s);
-        else orc_softmax_fast(scores + (int64_t)r * s, s);
-      }
+      softmax_rows(scores, s, j->math_mode, j->spawned ? 1 : g_threads);
       orc_sgemm(0, 0, s, hd, s, 1.0f, scores, s, j->v + off, c, 0.0f,
                 j->out + off, c);
     }

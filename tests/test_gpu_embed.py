@@ -93,6 +93,25 @@ def test_embed_oracle_sample(nomic_model, orc):
     assert cos.min() >= 0.999
 
 
+def test_fp16_output_is_rne_of_fp32(nomic_model, fl):
+    """The fp16 transport (processOutput's Cast(Float16) + ExtractBytes,
+    embeddings.go:256-286): fl_model_forward_ex / fl_model_embed_ex with
+    FL_F16 deliver exactly numpy's round-to-nearest-even of the fp32 vectors."""
+    cfg, _w, m = nomic_model
+    lengths = synth.ragged_lengths(70, seed=31)
+    ids = synth.make_ids(lengths, seed=32)
+    f32 = m.forward(ids, lengths)
+    f16 = m.forward(ids, lengths, out_dtype=fl.F16)
+    assert f16.dtype == np.float16
+    np.testing.assert_array_equal(f16.view(np.uint16), f32.astype(np.float16).view(np.uint16))
+    e32, _n, nb = m.embed(ids, lengths, max_seqs=16, max_tokens=2048)
+    e16, _n, nb16 = m.embed(ids, lengths, max_seqs=16, max_tokens=2048, out_dtype=fl.F16)
+    assert nb16 == nb > 2
+    np.testing.assert_array_equal(e16.view(np.uint16), e32.astype(np.float16).view(np.uint16))
+    with pytest.raises(fl.FletcherError):
+        m.forward(ids, lengths, out_dtype=fl.BF16)
+
+
 def test_embed_edge_cases(nomic_model):
     cfg, _w, m = nomic_model
     out, nan, nb = m.embed(np.zeros(0, np.int64), np.zeros(0, np.int64))

@@ -58,7 +58,7 @@ def sample_rows(lengths, k):
 def oracle_rows(orc, cfg, ids, lengths, rows, math_mode=0):
     starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
     sub_ids = np.concatenate([ids[starts[r]:starts[r] + lengths[r]] for r in rows])
-    orc.set_threads(8)
+    orc.set_threads(16)
     return orc.forward(cfg, weights_for(cfg), sub_ids, np.asarray(lengths)[rows], math_mode)
 
 
@@ -106,25 +106,41 @@ def test_config2_bert_base_f16(ctx, fl, orc):
     ids = synth.make_ids(lengths)
     log("config2 gpu")
     got = run_gpu(fl, ctx, w.cfg, fl.F16, fl.MATH_EXACT, ids, lengths)
-    rows = sample_rows(lengths, 4)
+    rows = list(range(0, 256, 32)) + [255]
     want = oracle_rows(orc, w.cfg, ids, lengths, rows)
     c = cosines(got[rows], want)
-    log(f"config2 min cos {c.min():.6f}")
+    log(f"config2 min cos {c.min():.6f} over {len(rows)} rows")
     assert c.min() >= COS_F16
     assert np.isfinite(got).all()
 
 
 def test_config3_nomic_f16(ctx, fl, orc):
-    """Config 3 (the north-star workload): Nomic, B256 x S512, fp16."""
+    """Config 3 (the north-star workload): Nomic, B256 x S512, fp16.  Every
+    16th sequence (17 rows, one in each 16-sequence = 8192-token stretch of
+    the GEMMs' row tiles) against the oracle; two 32-sequence slices rerun
+    alone on the GPU must reproduce their rows of the full batch."""
     w = synth.WORKLOADS["nomic-b256-s512-f16"]
     lengths = w.lengths()
     ids = synth.make_ids(lengths)
-    log("config3 gpu")
-    got = run_gpu(fl, ctx, w.cfg, fl.F16, fl.MATH_EXACT, ids, lengths)
-    rows = sample_rows(lengths, 2)[:2]
+    starts = np.concatenate([[0], np.cumsum(lengths)])
+    m = fl.Model(ctx, w.cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(weights_for(w.cfg))
+        log("config3 gpu full batch")
+        got = m.forward(ids, lengths)
+        assert m.status() == (False, False)
+        for a, b in ((64, 96), (160, 192)):
+            part = m.forward(ids[starts[a]:starts[b]], lengths[a:b])
+            c = cosines(part, got[a:b])
+            log(f"config3 rows {a}-{b - 1} alone vs full batch: min cos {c.min():.7f}")
+            assert c.min() >= 0.99999
+    finally:
+        m.close()
+    rows = list(range(0, 256, 16)) + [255]
+    log(f"config3 oracle on {len(rows)} rows")
     want = oracle_rows(orc, w.cfg, ids, lengths, rows)
     c = cosines(got[rows], want)
-    log(f"config3 min cos {c.min():.6f}")
+    log(f"config3 min cos {c.min():.6f} over {len(rows)} rows")
     assert c.min() >= COS_F16
     np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
 
@@ -158,30 +174,34 @@ def test_config4_ragged_f16(ctx, fl, orc):
 
 
 def test_config5_long_context_f16(ctx, fl, orc):
-    """Config 5: B16 x S8192.  Full 12-layer batch on the GPU (finite, unit
-    norm, row 0 equal to a batch of one); 1-layer parity against the oracle at
-    the full 8192 length."""
+    """Config 5: B16 x S8192, full 12 layers.  One whole 8192-token row
+    against the oracle; three rows rerun as their own batch on the GPU must
+    reproduce their rows of the full batch."""
     w = synth.WORKLOADS["nomic-b16-s8192-f16"]
     lengths = w.lengths()
     ids = synth.make_ids(lengths)
+    starts = np.concatenate([[0], np.cumsum(lengths)])
+    pick = [3, 9, 15]
+    sub_ids = np.concatenate([ids[starts[r]:starts[r + 1]] for r in pick])
     m = fl.Model(ctx, w.cfg, dtype=fl.F16, math=fl.MATH_EXACT)
     try:
         m.load(weights_for(w.cfg))
         log("config5 gpu full batch")
         got = m.forward(ids, lengths)
-        one = m.forward(ids[:lengths[0]], lengths[:1])
+        assert m.status() == (False, False)
+        part = m.forward(sub_ids, lengths[pick])
     finally:
         m.close()
     assert np.isfinite(got).all()
     np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
-    assert cosines(one, got[:1]).min() >= 0.99999
-
-    cfg1 = synth.nomic(layers=1)
-    got1 = run_gpu(fl, ctx, cfg1, fl.F16, fl.MATH_EXACT, ids[:8192], np.array([8192]))
-    log("config5 oracle, 1 layer x 8192")
-    want1 = orc.forward(cfg1, weights_for(cfg1), ids[:8192], np.array([8192]))
-    c = cosines(got1, want1)
-    log(f"config5 1-layer cos {c.min():.6f}")
+    c = cosines(part, got[pick])
+    log(f"config5 rows {pick} alone vs full batch: min cos {c.min():.7f}")
+    assert c.min() >= 0.99999
+    row = 5
+    log("config5 oracle, 12 layers x 8192 tokens")
+    want = oracle_rows(orc, w.cfg, ids, lengths, [row])
+    c = cosines(got[[row]], want)
+    log(f"config5 row {row} cos {c.min():.6f}")
     assert c.min() >= COS_F16
 
 
