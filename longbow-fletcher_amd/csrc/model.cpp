@@ -433,7 +433,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
     {
       ProfScope ps(m, P_QKV);
       GemmEpilogue e;
-      e.bias = w.bqkv;
+      e.bias = m->cfg.has_bias ? w.bqkv : nullptr;
       e.layout = m->lay_qkv;
       if (m->rope && m->rope_fused) {
         e.kind = EPI_ROPE;
@@ -473,7 +473,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
     {
       ProfScope ps(m, P_O);
       GemmEpilogue e;
-      e.bias = w.bo;
+      e.bias = m->cfg.has_bias ? w.bo : nullptr;
       e.layout = m->lay_o;
       M_ST(gemm(m, m->mfma_o, m->CTX, w.wo, m->TMP, Ti, H, H, e));
     }
@@ -485,7 +485,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
     {
       ProfScope ps(m, P_UP);
       GemmEpilogue e;
-      e.bias = w.bi;
+      e.bias = m->cfg.has_bias ? w.bi : nullptr;
       e.math = m->cfg.math;
       e.layout = m->lay_up;
       if (m->swiglu) {
@@ -507,7 +507,7 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
     {
       ProfScope ps(m, P_DOWN);
       GemmEpilogue e;
-      e.bias = w.bd;
+      e.bias = m->cfg.has_bias ? w.bd : nullptr;
       e.layout = m->lay_down;
       e.a_tiled = m->ffn_tiled;
       // With X tiled, the SwiGLU output's padding rows come from X's padding
@@ -744,6 +744,14 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
   } else {
     LayerW& L = m->layers[layer];
     const size_t esz = m->esz;
+    // A model created without biases (Nomic) never reads them: a projection
+    // bias that is not zero is refused, as the weight-file loaders do.
+    const bool proj_bias = field == "q_b" || field == "k_b" || field == "v_b" ||
+                           field == "o_b" || field == "inter_b" || field == "out_b";
+    if (proj_bias && !m->cfg.has_bias)
+      for (int64_t i = 0; i < n; ++i)
+        if (data[i] != 0.0f)
+          return fail(FL_ERR_INVALID, "weight " + nm + ": the model was created without biases");
     if (field == "q_w" || field == "k_w" || field == "v_w") {
       M_ST(expect(H * H));
       const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);

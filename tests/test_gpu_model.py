@@ -276,6 +276,20 @@ def test_model_errors(ctx, fl):
         m.close()
 
 
+def test_bias_free_model_rejects_nonzero_bias_weight(ctx, fl):
+    """A model created without biases (Nomic) adds none in its GEMM epilogues;
+    a projection bias that is not zero is refused rather than ignored."""
+    cfg = synth.nomic(layers=1, vocab_size=2000, max_pos=512)
+    m = fl.Model(ctx, cfg, dtype=fl.F16)
+    try:
+        for name, n in (("o_b.0", cfg.hidden), ("inter_b.0", 2 * cfg.intermediate)):
+            m.set_weight(name, np.zeros(n, np.float32))
+            with pytest.raises(fl.FletcherError):
+                m.set_weight(name, np.full(n, 0.5, np.float32))
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("pool", ["mean_l2", "cls"])
 def test_last_hidden_row_major(ctx, fl, orc, pool):
     """The hidden states the library hands back are row-major whatever layout
