@@ -1515,10 +1515,25 @@ constexpr bool pp_epilogue_ok(int epi, int math) {
          (math == MATH_EXACT && (epi == EPI_SWIGLU || epi == EPI_GELU));
 }
 
+// Workgroups of a persistent launch over ntiles tiles: the fewest that take
+// the same number of rounds of tiles as one per CU (a multiple of 8 where
+// that stays within the CUs, for the XCD-chunked tile order).  The kernel
+// takes as long as with one workgroup per CU, and the CUs it leaves free run
+// other streams' work (fl_model_embed runs two batches at once).
+static int persistent_grid(int ntiles) {
+  const int cus = cu_count();
+  if (ntiles <= 0) return 1;
+  const int rounds = (ntiles + cus - 1) / cus;
+  int grid = (ntiles + rounds - 1) / rounds;
+  const int g8 = (grid + 7) / 8 * 8;
+  if (g8 <= cus && (ntiles + g8 - 1) / g8 == rounds) grid = g8;
+  return grid;
+}
+
 template <typename T, int EPI, int MATH>
 static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
-  const int grid = std::min(ntiles, cu_count());
+  const int grid = persistent_grid(ntiles);
   // SwiGLU's output staging area (8 waves x FL_GEMM_PP_SPREAD KB) takes the
   // LDS of one stage when it exceeds the 32 KB that four stages leave.
   constexpr int NS = EPI == EPI_SWIGLU && FL_GEMM_PP_SPREAD > 4 ? FL_GEMM_PP_NS - 1 : FL_GEMM_PP_NS;
@@ -1540,7 +1555,7 @@ static bool gemm_w4_ok(const GemmParams& p) {
 template <typename T, int EPI, int MATH>
 static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
-  const int grid = std::min(ntiles, cu_count());
+  const int grid = persistent_grid(ntiles);
   hipLaunchKernelGGL((gemm_w4_kernel<T, EPI, MATH, 4>), dim3(grid), dim3(256), 0, s,
                      p, ntiles);
   return hipGetLastError();

@@ -47,6 +47,55 @@ struct LayerW {
 
 enum ProfClass { P_EMBED = 0, P_QKV, P_ATTN, P_O, P_LN, P_UP, P_DOWN, P_POOL };
 
+// Pinned host staging of a batch's metadata (attention work list,
+// cu_seqlens, positions), two slots per lane used in turn so a batch's upload
+// never waits for the previous batch's kernels: a slot is refilled only after
+// its copy (event) has completed.
+struct Staging {
+  void* host = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+
+// Everything one batch's forward reads and writes besides the weights: the
+// activation buffers, the batch metadata and the stream the forward runs on.
+// Lane 0 runs on the context stream and serves every entry point; the
+// batching loop of fl_model_embed also uses lane 1 on a stream of its own, so
+// consecutive batches run concurrently and one batch's kernels fill the CUs
+// the other's leave idle (a 16384-token batch gives its N = 768 GEMMs 192
+// tiles for 256 CUs).
+struct Lane {
+  hipStream_t stream = nullptr;
+  // activations (capacity in tokens / sequences)
+  int64_t cap_tokens = 0;
+  int cap_seq = 0;
+  size_t cap_work = 0;
+  size_t cap_part = 0;
+  void* X = nullptr;
+  void* QKV = nullptr;  // also holds the FFN intermediate
+  void* CTX = nullptr;
+  void* TMP = nullptr;
+  void* G2 = nullptr;   // [T, 2I] unfused SwiGLU product (only without the fused epilogue)
+  int* ids32 = nullptr;
+  int* pos32 = nullptr;
+  int* cu = nullptr;
+  AttnWork* work = nullptr;
+  float* part = nullptr;
+  float* cls = nullptr;
+  float* out = nullptr;
+  uint16_t* out16 = nullptr;  // fp16 copy of `out` (FL_F16 output)
+  int* flags = nullptr;       // [0] NaN in pooled output, [1] id out of range
+  Staging meta[2];
+  int meta_slot = 0;
+  std::vector<int64_t> last_lengths;
+  int64_t T = 0;
+  int n_work = 0, max_len = 0, waves = 4;
+  int qblocks = 1;  // query blocks of the longest sequence (flash work items per head)
+  const float2* rope_cs = nullptr;
+  const float2* rope_cs_q = nullptr;  // rope_cs * scale * log2(e), for a pre-scaled Q
+};
+
 }  // namespace fl
 
 using namespace fl;
@@ -72,40 +121,11 @@ struct fl_model {
   float* pool_b = nullptr;
   std::unordered_map<void*, size_t> owned;  // device buffers and their sizes
 
-  // activations (capacity in tokens / sequences)
-  int64_t cap_tokens = 0;
-  int cap_seq = 0;
-  size_t cap_work = 0;
-  size_t cap_part = 0;
-  void* X = nullptr;
-  void* QKV = nullptr;  // also holds the FFN intermediate
-  void* CTX = nullptr;
-  void* TMP = nullptr;
-  void* G2 = nullptr;   // [T, 2I] unfused SwiGLU product (only without the fused epilogue)
-  int* ids32 = nullptr;
-  int* pos32 = nullptr;
-  int* cu = nullptr;
-  AttnWork* work = nullptr;
-  float* part = nullptr;
-  float* cls = nullptr;
-  float* out = nullptr;
-  uint16_t* out16 = nullptr;  // fp16 copy of `out` (FL_F16 output)
-  int* flags = nullptr;  // [0] NaN in pooled output, [1] id out of range
-
-  // Pinned host staging of the per-batch metadata (attention work list,
-  // cu_seqlens, positions), two slots used in turn so a batch's upload never
-  // waits for the previous batch's kernels: a slot is refilled only after
-  // its copy (event) has completed.
-  struct Staging {
-    void* host = nullptr;
-    size_t cap = 0;
-    hipEvent_t done = nullptr;
-    bool pending = false;
-  } meta[2];
-  int meta_slot = 0;
+  // Lane 0: the context stream; lane 1: fl_model_embed's second stream.
+  Lane lane[2];
 
   // fl_model_embed's pipeline: ids go up on `up`, pooled vectors and the
-  // batch's flags come back on `down`, forwards run on the context stream.
+  // batch's flags come back on `down`, forwards run on the lanes' streams.
   struct Pipe {
     hipStream_t up = nullptr, down = nullptr;
     int32_t* ids_pin[2] = {nullptr, nullptr};
@@ -120,10 +140,6 @@ struct fl_model {
     int cap_seq = 0;
   } pipe;
 
-  std::vector<int64_t> last_lengths;
-  int64_t T = 0;
-  int n_work = 0, max_len = 0, waves = 4;
-  int qblocks = 1;            // query blocks of the longest sequence (flash work items per head)
   bool q_prescaled = false;   // QKV epilogue multiplies Q by scale * log2(e) for the flash kernel
   // The SwiGLU output (FFN-down's activations) is kept in the tiled layout
   // (tiled_act_offset), so FFN-down streams it in contiguous 16 KB blocks.
@@ -132,8 +148,6 @@ struct fl_model {
   // activations) is kept tiled too; activation buffers then have rows up to
   // a multiple of 256 and the GEMMs reading X write their padding rows.
   bool x_tiled = false;
-  const float2* rope_cs = nullptr;
-  const float2* rope_cs_q = nullptr;  // rope_cs * scale * log2(e), for a pre-scaled Q
 
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;
@@ -203,18 +217,19 @@ hipEvent_t next_event(fl_model* m) {
   return m->ev_pool[m->ev_next++];
 }
 
+// Kernel timing of lane 0's forwards (the context stream).
 struct ProfScope {
   fl_model* m;
   int cls;
   hipEvent_t a = nullptr;
-  ProfScope(fl_model* mm, int c) : m(mm), cls(c) {
-    if (m->prof) {
+  ProfScope(fl_model* mm, const Lane& L, int c) : m(mm), cls(c) {
+    if (m->prof && L.stream == m->ctx->stream) {
       a = next_event(m);
       if (a) (void)hipEventRecord(a, m->ctx->stream);
     }
   }
   ~ProfScope() {
-    if (m->prof && a) {
+    if (a) {
       hipEvent_t b = next_event(m);
       if (b) {
         (void)hipEventRecord(b, m->ctx->stream);
@@ -248,59 +263,59 @@ bool mfma_shape_ok(int dtype, int N, int K) {
 // Grows the activation buffers.  Capacities drop to 0 and old buffers are
 // freed (pointers cleared) before anything is allocated, so an allocation
 // that fails leaves a model whose next call reallocates from scratch.
-int ensure_capacity(fl_model* m, int64_t T, int nseq, size_t nwork, size_t part_elems) {
-  if (T > m->cap_tokens) {
-    M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    m->cap_tokens = 0;
-    m->last_lengths.clear();
-    untrack_free(m, m->X);
-    untrack_free(m, m->QKV);
-    untrack_free(m, m->CTX);
-    untrack_free(m, m->TMP);
-    untrack_free(m, m->G2);
-    untrack_free(m, m->ids32);
-    untrack_free(m, m->pos32);
+int ensure_capacity(fl_model* m, Lane& L, int64_t T, int nseq, size_t nwork, size_t part_elems) {
+  if (T > L.cap_tokens) {
+    M_CHECK(hipStreamSynchronize(L.stream));
+    L.cap_tokens = 0;
+    L.last_lengths.clear();
+    untrack_free(m, L.X);
+    untrack_free(m, L.QKV);
+    untrack_free(m, L.CTX);
+    untrack_free(m, L.TMP);
+    untrack_free(m, L.G2);
+    untrack_free(m, L.ids32);
+    untrack_free(m, L.pos32);
     // Rows rounded up to whole 256-row tiles (tiled activations, padded GEMM outputs).
     int64_t cap = (std::max<int64_t>(T, 256) + 255) / 256 * 256;
     const int64_t wide = std::max<int64_t>(3 * m->H, m->Ni);
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->X));
-    M_ST(track_alloc(m, (size_t)cap * wide * m->esz, m->QKV));
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->CTX));
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, m->TMP));
-    if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, m->G2));
-    M_ST(track_alloc(m, (size_t)cap * 4, m->ids32));
-    M_ST(track_alloc(m, (size_t)cap * 4, m->pos32));
-    m->cap_tokens = cap;
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.X));
+    M_ST(track_alloc(m, (size_t)cap * wide * m->esz, L.QKV));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.CTX));
+    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.TMP));
+    if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, L.G2));
+    M_ST(track_alloc(m, (size_t)cap * 4, L.ids32));
+    M_ST(track_alloc(m, (size_t)cap * 4, L.pos32));
+    L.cap_tokens = cap;
   }
-  if (nseq > m->cap_seq) {
-    M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    m->cap_seq = 0;
-    m->last_lengths.clear();
-    untrack_free(m, m->cu);
-    untrack_free(m, m->cls);
-    untrack_free(m, m->out);
-    untrack_free(m, m->out16);
+  if (nseq > L.cap_seq) {
+    M_CHECK(hipStreamSynchronize(L.stream));
+    L.cap_seq = 0;
+    L.last_lengths.clear();
+    untrack_free(m, L.cu);
+    untrack_free(m, L.cls);
+    untrack_free(m, L.out);
+    untrack_free(m, L.out16);
     const int cap = std::max(nseq, 64);
-    M_ST(track_alloc(m, (size_t)(cap + 1) * 4, m->cu));
-    M_ST(track_alloc(m, (size_t)cap * m->H * 4, m->cls));
-    M_ST(track_alloc(m, (size_t)cap * m->H * 4, m->out));
-    M_ST(track_alloc(m, (size_t)cap * m->H * 2, m->out16));
-    m->cap_seq = cap;
+    M_ST(track_alloc(m, (size_t)(cap + 1) * 4, L.cu));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, L.cls));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 4, L.out));
+    M_ST(track_alloc(m, (size_t)cap * m->H * 2, L.out16));
+    L.cap_seq = cap;
   }
-  if (nwork > m->cap_work) {
-    M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    m->cap_work = 0;
-    m->last_lengths.clear();
-    untrack_free(m, m->work);
-    M_ST(track_alloc(m, nwork * sizeof(AttnWork), m->work));
-    m->cap_work = nwork;
+  if (nwork > L.cap_work) {
+    M_CHECK(hipStreamSynchronize(L.stream));
+    L.cap_work = 0;
+    L.last_lengths.clear();
+    untrack_free(m, L.work);
+    M_ST(track_alloc(m, nwork * sizeof(AttnWork), L.work));
+    L.cap_work = nwork;
   }
-  if (part_elems > m->cap_part) {
-    M_CHECK(hipStreamSynchronize(m->ctx->stream));
-    m->cap_part = 0;
-    untrack_free(m, m->part);
-    M_ST(track_alloc(m, part_elems * 4, m->part));
-    m->cap_part = part_elems;
+  if (part_elems > L.cap_part) {
+    M_CHECK(hipStreamSynchronize(L.stream));
+    L.cap_part = 0;
+    untrack_free(m, L.part);
+    M_ST(track_alloc(m, part_elems * 4, L.part));
+    L.cap_part = part_elems;
   }
   return FL_OK;
 }
@@ -309,7 +324,7 @@ constexpr int kPoolRows = 64;
 
 // Uploads cu_seqlens, per-token positions and the attention work list when
 // the batch's lengths differ from the previous call.
-int prepare(fl_model* m, const int64_t* lengths, int nseq) {
+int prepare(fl_model* m, Lane& L, const int64_t* lengths, int nseq) {
   int64_t T = 0;
   int max_len = 0;
   for (int b = 0; b < nseq; ++b) {
@@ -326,15 +341,15 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
   if (fast_attn)
     for (int b = 0; b < nseq; ++b) nwork += (size_t)m->heads * ((lengths[b] + bq - 1) / bq);
   const size_t part = (size_t)nseq * ((max_len + kPoolRows - 1) / kPoolRows) * m->H;
-  M_ST(ensure_capacity(m, T, nseq, std::max<size_t>(nwork, 1), part));
+  M_ST(ensure_capacity(m, L, T, nseq, std::max<size_t>(nwork, 1), part));
 
-  const bool same = (int)m->last_lengths.size() == nseq &&
-                    std::equal(m->last_lengths.begin(), m->last_lengths.end(), lengths);
+  const bool same = (int)L.last_lengths.size() == nseq &&
+                    std::equal(L.last_lengths.begin(), L.last_lengths.end(), lengths);
   if (!same) {
     // Layout of a staging slot: work list (16-byte entries) | cu | pos.
     const size_t need = nwork * sizeof(AttnWork) + (size_t)(nseq + 1) * 4 + (size_t)T * 4;
-    fl_model::Staging& sg = m->meta[m->meta_slot];
-    m->meta_slot ^= 1;
+    Staging& sg = L.meta[L.meta_slot];
+    L.meta_slot ^= 1;
     if (sg.pending) {
       M_CHECK(hipEventSynchronize(sg.done));
       sg.pending = false;
@@ -373,36 +388,36 @@ int prepare(fl_model* m, const int64_t* lengths, int nseq) {
     }
     if (m->rope) {
       int st;
-      m->rope_cs = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st);
+      L.rope_cs = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st);
       if (st) return st;
       if (m->q_prescaled) {
-        m->rope_cs_q = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st,
+        L.rope_cs_q = rope_table(m->ctx, m->cfg.rope_base, m->hd / 2, max_len, &st,
                                   attn_scale(m->hd) * kLog2e);
         if (st) return st;
       }
     }
     // Stream-ordered after the previous batch's kernels, which read the same
     // device buffers.
-    hipStream_t s = m->ctx->stream;
-    M_CHECK(hipMemcpyAsync(m->cu, cu, (nseq + 1) * 4, hipMemcpyHostToDevice, s));
-    M_CHECK(hipMemcpyAsync(m->pos32, pos, (size_t)T * 4, hipMemcpyHostToDevice, s));
+    hipStream_t s = L.stream;
+    M_CHECK(hipMemcpyAsync(L.cu, cu, (nseq + 1) * 4, hipMemcpyHostToDevice, s));
+    M_CHECK(hipMemcpyAsync(L.pos32, pos, (size_t)T * 4, hipMemcpyHostToDevice, s));
     if (n_work)
-      M_CHECK(hipMemcpyAsync(m->work, work, n_work * sizeof(AttnWork), hipMemcpyHostToDevice, s));
+      M_CHECK(hipMemcpyAsync(L.work, work, n_work * sizeof(AttnWork), hipMemcpyHostToDevice, s));
     M_CHECK(hipEventRecord(sg.done, s));
     sg.pending = true;
-    m->last_lengths.assign(lengths, lengths + nseq);
-    m->n_work = (int)n_work;
-    m->waves = waves;
-    m->qblocks = (max_len + bq - 1) / bq;
+    L.last_lengths.assign(lengths, lengths + nseq);
+    L.n_work = (int)n_work;
+    L.waves = waves;
+    L.qblocks = (max_len + bq - 1) / bq;
   }
-  m->T = T;
-  m->max_len = max_len;
+  L.T = T;
+  L.max_len = max_len;
   return FL_OK;
 }
 
-int gemm(fl_model* m, bool mfma, const void* A, const void* W, void* C, int M, int N, int K,
-         const GemmEpilogue& epi) {
-  hipStream_t s = m->ctx->stream;
+int gemm(fl_model* m, const Lane& L, bool mfma, const void* A, const void* W, void* C, int M,
+         int N, int K, const GemmEpilogue& epi) {
+  hipStream_t s = L.stream;
   if (mfma) {
     M_CHECK(launch_gemm_nt(m->dtype, A, K, W, K, C, epi.kind == EPI_SWIGLU ? N / 2 : N, M, N, K,
                            epi, s));
@@ -414,76 +429,76 @@ int gemm(fl_model* m, bool mfma, const void* A, const void* W, void* C, int M, i
   return FL_OK;
 }
 
-// The forward on device-resident ids (m->ids32 or caller memory) into d_out.
-int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
-  hipStream_t s = m->ctx->stream;
-  const int64_t T = m->T;
+// The forward on device-resident ids (L.ids32 or caller memory) into d_out, on L's stream.
+int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* flags) {
+  hipStream_t s = L.stream;
+  const int64_t T = L.T;
   const int H = m->H, dt = m->dtype;
   const int Ti = (int)T;
   M_CHECK(hipMemsetAsync(flags, 0, 8, s));
   {
-    ProfScope ps(m, P_EMBED);
-    M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : m->pos32, m->word,
+    ProfScope ps(m, L, P_EMBED);
+    M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : L.pos32, m->word,
                             m->rope ? nullptr : m->pos, m->type, Ti, H, m->emb_g, m->emb_b,
-                            m->cfg.ln_eps, m->cfg.vocab_size, flags + 1, m->X, s,
+                            m->cfg.ln_eps, m->cfg.vocab_size, flags + 1, L.X, s,
                             m->x_tiled));
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const LayerW& w = m->layers[l];
     {
-      ProfScope ps(m, P_QKV);
+      ProfScope ps(m, L, P_QKV);
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bqkv : nullptr;
       e.layout = m->lay_qkv;
       if (m->rope && m->rope_fused) {
         e.kind = EPI_ROPE;
-        e.rope_cs = m->rope_cs;
-        e.pos = m->pos32;
+        e.rope_cs = L.rope_cs;
+        e.pos = L.pos32;
         e.rope_cols = 2 * H;
       }
       if (m->q_prescaled) {
         e.q_cols = H;
         e.q_scale = attn_scale(m->hd) * kLog2e;
-        e.rope_cs_q = m->rope_cs_q;
+        e.rope_cs_q = L.rope_cs_q;
       }
       e.a_tiled = e.c_padded = m->x_tiled;
-      M_ST(gemm(m, m->mfma_qkv, m->X, w.wqkv, m->QKV, Ti, 3 * H, H, e));
+      M_ST(gemm(m, L, m->mfma_qkv, L.X, w.wqkv, L.QKV, Ti, 3 * H, H, e));
       if (m->rope && !m->rope_fused)
-        M_CHECK(launch_rope(dt, m->QKV, Ti, 2 * m->heads, m->hd, 3 * H, m->pos32, m->rope_cs, s));
+        M_CHECK(launch_rope(dt, L.QKV, Ti, 2 * m->heads, m->hd, 3 * H, L.pos32, L.rope_cs, s));
     }
     {
-      ProfScope ps(m, P_ATTN);
+      ProfScope ps(m, L, P_ATTN);
       const float scale = attn_scale(m->hd);
-      const char* q = (const char*)m->QKV;
+      const char* q = (const char*)L.QKV;
       const void* k = q + (size_t)H * m->esz;
       const void* v = q + (size_t)2 * H * m->esz;
       // XCD groups of two (sequence, head) pairs' query blocks: measured 2%
       // faster than one pair at 512 tokens (the kernel clamps groups at 32).
       if ((m->hd == 64 || m->hd == 32) && dt != FL_F32)
-        M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, m->CTX, H, m->cu, m->work, m->n_work,
-                                       m->hd, scale, m->waves, m->q_prescaled, 2 * m->qblocks, s));
+        M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, L.CTX, H, L.cu, L.work, L.n_work,
+                                       m->hd, scale, L.waves, m->q_prescaled, 2 * L.qblocks, s));
       else if (m->hd == 64)
         M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
-                                     (float*)m->CTX, H, m->cu, m->work, m->n_work, scale,
+                                     (float*)L.CTX, H, L.cu, L.work, L.n_work, scale,
                                      m->cfg.math, s));
       else
-        M_CHECK(launch_attention_generic(dt, q, k, v, 3 * H, m->CTX, H, m->cu, nseq, m->max_len,
+        M_CHECK(launch_attention_generic(dt, q, k, v, 3 * H, L.CTX, H, L.cu, nseq, L.max_len,
                                          m->heads, m->hd, scale, m->cfg.math, s));
     }
     {
-      ProfScope ps(m, P_O);
+      ProfScope ps(m, L, P_O);
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bo : nullptr;
       e.layout = m->lay_o;
-      M_ST(gemm(m, m->mfma_o, m->CTX, w.wo, m->TMP, Ti, H, H, e));
+      M_ST(gemm(m, L, m->mfma_o, L.CTX, w.wo, L.TMP, Ti, H, H, e));
     }
     {
-      ProfScope ps(m, P_LN);
-      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s,
+      ProfScope ps(m, L, P_LN);
+      M_CHECK(launch_layernorm(dt, L.X, L.TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s,
                                m->x_tiled));
     }
     {
-      ProfScope ps(m, P_UP);
+      ProfScope ps(m, L, P_UP);
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bi : nullptr;
       e.math = m->cfg.math;
@@ -493,19 +508,19 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
           e.kind = EPI_SWIGLU;
           e.out_tiled = m->ffn_tiled;
           e.a_tiled = m->x_tiled;
-          M_ST(gemm(m, true, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
+          M_ST(gemm(m, L, true, L.X, w.wi, L.QKV, Ti, m->Ni, H, e));
         } else {
           // Unfused: [T, 2I] product, then silu(gate) * up into QKV.
-          M_ST(gemm(m, false, m->X, w.wi, m->G2, Ti, m->Ni, H, e));
-          M_CHECK(launch_swiglu(dt, m->G2, Ti, m->I, m->QKV, m->cfg.math, s));
+          M_ST(gemm(m, L, false, L.X, w.wi, L.G2, Ti, m->Ni, H, e));
+          M_CHECK(launch_swiglu(dt, L.G2, Ti, m->I, L.QKV, m->cfg.math, s));
         }
       } else {
         e.kind = EPI_GELU;
-        M_ST(gemm(m, m->mfma_up, m->X, w.wi, m->QKV, Ti, m->Ni, H, e));
+        M_ST(gemm(m, L, m->mfma_up, L.X, w.wi, L.QKV, Ti, m->Ni, H, e));
       }
     }
     {
-      ProfScope ps(m, P_DOWN);
+      ProfScope ps(m, L, P_DOWN);
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bd : nullptr;
       e.layout = m->lay_down;
@@ -513,29 +528,43 @@ int run(fl_model* m, const int* d_ids, int nseq, float* d_out, int* flags) {
       // With X tiled, the SwiGLU output's padding rows come from X's padding
       // rows (no copies of row T-1): FFN-down writes its own padding rows.
       e.c_padded = m->x_tiled;
-      M_ST(gemm(m, m->mfma_down, m->QKV, w.wd, m->TMP, Ti, H, m->I, e));
+      M_ST(gemm(m, L, m->mfma_down, L.QKV, w.wd, L.TMP, Ti, H, m->I, e));
     }
     {
-      ProfScope ps(m, P_LN);
-      M_CHECK(launch_layernorm(dt, m->X, m->TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s,
+      ProfScope ps(m, L, P_LN);
+      M_CHECK(launch_layernorm(dt, L.X, L.TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s,
                                m->x_tiled));
     }
   }
   {
-    ProfScope ps(m, P_POOL);
+    ProfScope ps(m, L, P_POOL);
     if (m->cfg.pool == FL_POOL_CLS_TANH) {
       // BertPooler (bert.go:441-488) in fp32 (bert.go:459-476 forces fp32 for fp16 weights).
-      M_CHECK(launch_gather_cls(dt, m->X, H, m->cu, nseq, m->cls, s, m->x_tiled));
-      M_CHECK(launch_gemm_generic(FL_F32, 0, 0, nseq, H, H, 1.0f, m->cls, H, m->pool_w, H, d_out,
+      M_CHECK(launch_gather_cls(dt, L.X, H, L.cu, nseq, L.cls, s, m->x_tiled));
+      M_CHECK(launch_gemm_generic(FL_F32, 0, 0, nseq, H, H, 1.0f, L.cls, H, m->pool_w, H, d_out,
                                   H, m->pool_b, FL_ACT_TANH, m->cfg.math, s));
       M_CHECK(launch_has_nan(d_out, FL_F32, (int64_t)nseq * H, flags, s));
     } else {
-      M_CHECK(launch_mean_pool_staged(dt, m->X, H, m->cu, nseq, m->max_len,
-                                      m->cfg.pool == FL_POOL_MEAN_L2, m->part, d_out, flags,
+      M_CHECK(launch_mean_pool_staged(dt, L.X, H, L.cu, nseq, L.max_len,
+                                      m->cfg.pool == FL_POOL_MEAN_L2, L.part, d_out, flags,
                                       kPoolRows, s, m->x_tiled));
     }
   }
   return FL_OK;
+}
+
+// Lane 0 runs on the context stream (looked up at every entry: the context
+// owns it).
+Lane& lane0(fl_model* m) {
+  m->lane[0].stream = m->ctx->stream;
+  return m->lane[0];
+}
+
+void free_staging(Staging& sg) {
+  if (sg.pending && sg.done) (void)hipEventSynchronize(sg.done);
+  if (sg.host) (void)hipHostFree(sg.host);
+  if (sg.done) (void)hipEventDestroy(sg.done);
+  sg = Staging{};
 }
 
 }  // namespace
@@ -643,7 +672,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     if ((st = fill_f32(&m->pool_w, H * H, 0.f)) || (st = fill_f32(&m->pool_b, H, 0.f))) break;
     void* f;
     if ((st = zeros(&f, 256))) break;
-    m->flags = (int*)f;
+    m->lane[0].flags = (int*)f;
   } while (0);
   if (st) {
     free_owned(m);
@@ -661,15 +690,16 @@ int fl_model_free(fl_model* m) {
     (void)activate(m->ctx);
     (void)hipStreamSynchronize(m->ctx->stream);
     fl_model::Pipe& P = m->pipe;
-    for (hipStream_t st : {P.up, P.down})
+    for (hipStream_t st : {P.up, P.down, m->lane[1].stream})
       if (st) (void)hipStreamSynchronize(st);
     for (int k = 0; k < 2; ++k) {
-      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k], m->meta[k].host})
+      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
         if (h) (void)hipHostFree(h);
-      for (hipEvent_t e : {P.h2d[k], P.fwd[k], P.d2h[k], m->meta[k].done})
+      for (hipEvent_t e : {P.h2d[k], P.fwd[k], P.d2h[k]})
         if (e) (void)hipEventDestroy(e);
+      for (Lane& L : m->lane) free_staging(L.meta[k]);
     }
-    for (hipStream_t st : {P.up, P.down})
+    for (hipStream_t st : {P.up, P.down, m->lane[1].stream})
       if (st) (void)hipStreamDestroy(st);
     free_owned(m);
     for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
@@ -789,8 +819,9 @@ static bool valid_out_dtype(int dt) { return dt == FL_F32 || dt == FL_F16; }
 static int forward_common(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
                           int out_dtype, void* out) {
   if (nseq <= 0) return FL_OK;
-  M_ST(prepare(m, lengths, nseq));
-  const int64_t T = m->T;
+  Lane& L = lane0(m);
+  M_ST(prepare(m, L, lengths, nseq));
+  const int64_t T = L.T;
   std::vector<int> i32((size_t)T);
   for (int64_t t = 0; t < T; ++t) {
     // cpu_backend.go:500-502: out-of-range ids are an error.
@@ -799,14 +830,14 @@ static int forward_common(fl_model* m, const int64_t* ids, const int64_t* length
     i32[t] = (int)ids[t];
   }
   hipStream_t s = m->ctx->stream;
-  M_CHECK(hipMemcpyAsync(m->ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
-  M_ST(run(m, m->ids32, nseq, m->out, m->flags));
+  M_CHECK(hipMemcpyAsync(L.ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
+  M_ST(run(m, L, L.ids32, nseq, L.out, L.flags));
   const size_t n = (size_t)nseq * m->H;
   if (out_dtype == FL_F16) {
-    M_CHECK(launch_cast(m->out, FL_F32, m->out16, FL_F16, (int64_t)n, 0, s));
-    M_CHECK(hipMemcpyAsync(out, m->out16, n * 2, hipMemcpyDeviceToHost, s));
+    M_CHECK(launch_cast(L.out, FL_F32, L.out16, FL_F16, (int64_t)n, 0, s));
+    M_CHECK(hipMemcpyAsync(out, L.out16, n * 2, hipMemcpyDeviceToHost, s));
   } else {
-    M_CHECK(hipMemcpyAsync(out, m->out, n * 4, hipMemcpyDeviceToHost, s));
+    M_CHECK(hipMemcpyAsync(out, L.out, n * 4, hipMemcpyDeviceToHost, s));
   }
   M_CHECK(hipStreamSynchronize(s));
   return FL_OK;
@@ -862,9 +893,10 @@ int fl_model_forward_device(fl_model* m, const int32_t* d_ids, const int64_t* le
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
   if (nseq == 0) return FL_OK;
-  M_ST(prepare(m, lengths, nseq));
+  Lane& L = lane0(m);
+  M_ST(prepare(m, L, lengths, nseq));
   note_write(m->ctx, d_out);
-  return run(m, d_ids, nseq, d_out, m->flags);
+  return run(m, L, d_ids, nseq, d_out, L.flags);
 }
 
 int fl_model_embed(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq, int max_seqs,
@@ -915,18 +947,18 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
       return fail(FL_ERR_INVALID, "Gather index out of bounds");
 
   fl_model::Pipe& P = m->pipe;
+  Lane& L0 = lane0(m);
   hipStream_t cs = m->ctx->stream;
   if (!P.up) {
     M_CHECK(hipStreamCreateWithFlags(&P.up, hipStreamNonBlocking));
     M_CHECK(hipStreamCreateWithFlags(&P.down, hipStreamNonBlocking));
+    M_CHECK(hipStreamCreateWithFlags(&m->lane[1].stream, hipStreamNonBlocking));
     for (int k = 0; k < 2; ++k)
       for (hipEvent_t* e : {&P.h2d[k], &P.fwd[k], &P.d2h[k]})
         M_CHECK(hipEventCreateWithFlags(e, hipEventDisableTiming));
   }
   if (max_bt > P.cap_tok || max_bs > P.cap_seq) {
-    M_CHECK(hipStreamSynchronize(cs));
-    M_CHECK(hipStreamSynchronize(P.up));
-    M_CHECK(hipStreamSynchronize(P.down));
+    for (hipStream_t st : {cs, P.up, P.down, m->lane[1].stream}) M_CHECK(hipStreamSynchronize(st));
     const int64_t ct = std::max(max_bt, P.cap_tok);
     const int cq = std::max(max_bs, P.cap_seq);
     for (int k = 0; k < 2; ++k) {
@@ -957,11 +989,13 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     P.cap_seq = cq;
   }
 
-  // Batch b uses slot b & 1.  The host fills a slot's pinned ids only after
-  // that slot's previous batch has been copied back (so its upload is long
-  // done too), and copies results out of it at the same point: the host runs
-  // up to two batches ahead of the device, like the reference's double
-  // buffering of outputs (embeddings.go:766-775).
+  // Batch b uses slot and lane b & 1: consecutive batches compute on the two
+  // lanes' streams at the same time, each filling the CUs the other's
+  // kernels leave idle.  The host fills a slot's pinned ids only after that
+  // slot's previous batch has been copied back (so its upload and its
+  // forward are long done too), and copies results out of it at the same
+  // point: the host runs up to two batches ahead of the device, like the
+  // reference's double buffering of outputs (embeddings.go:766-775).
   const int64_t H = m->H;
   const size_t osz = out_dtype == FL_F16 ? 2 : 4;
   auto drain = [&](int b) -> int {
@@ -981,23 +1015,25 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     for (int64_t t = 0; t < pb.tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[pb.tok0 + t];
     M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)pb.tokens * 4, hipMemcpyHostToDevice, P.up));
     M_CHECK(hipEventRecord(P.h2d[k], P.up));
-    M_CHECK(hipStreamWaitEvent(cs, P.h2d[k], 0));
-    M_ST(prepare(m, lengths + pb.first, pb.count));
-    M_ST(run(m, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
+    Lane& L = m->lane[k];
+    M_CHECK(hipStreamWaitEvent(L.stream, P.h2d[k], 0));
+    M_ST(prepare(m, L, lengths + pb.first, pb.count));
+    M_ST(run(m, L, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
     const void* dev_out = P.out_dev[k];
     if (out_dtype == FL_F16) {
-      M_CHECK(launch_cast(P.out_dev[k], FL_F32, P.out16_dev[k], FL_F16, (int64_t)pb.count * H, 0, cs));
+      M_CHECK(launch_cast(P.out_dev[k], FL_F32, P.out16_dev[k], FL_F16, (int64_t)pb.count * H, 0,
+                          L.stream));
       dev_out = P.out16_dev[k];
     }
-    M_CHECK(hipEventRecord(P.fwd[k], cs));
+    M_CHECK(hipEventRecord(P.fwd[k], L.stream));
     M_CHECK(hipStreamWaitEvent(P.down, P.fwd[k], 0));
     M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)pb.count * H * osz, hipMemcpyDeviceToHost, P.down));
     M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, P.down));
     M_CHECK(hipEventRecord(P.d2h[k], P.down));
   }
   for (int b = std::max(0, nb - 2); b < nb; ++b) M_ST(drain(b));
-  // fl_model_status then reports the last batch.
-  M_CHECK(hipMemcpyAsync(m->flags, P.flags_dev[(nb - 1) & 1], 8, hipMemcpyDeviceToDevice, cs));
+  // fl_model_status then reports the last batch (drained, so its forward is done).
+  M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[(nb - 1) & 1], 8, hipMemcpyDeviceToDevice, cs));
   if (nbatches) *nbatches = nb;
   return FL_OK;
 }
@@ -1007,7 +1043,7 @@ int fl_model_status(fl_model* m, int* nan_in_output, int* bad_ids) {
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
   int h[2] = {0, 0};
-  M_CHECK(hipMemcpyAsync(h, m->flags, 8, hipMemcpyDeviceToHost, m->ctx->stream));
+  M_CHECK(hipMemcpyAsync(h, lane0(m).flags, 8, hipMemcpyDeviceToHost, m->ctx->stream));
   M_CHECK(hipStreamSynchronize(m->ctx->stream));
   if (nan_in_output) *nan_in_output = h[0] != 0;
   if (bad_ids) *bad_ids = h[1] != 0;
@@ -1018,15 +1054,16 @@ int fl_model_last_hidden(fl_model* m, float* out, int64_t n) {
   if (!m || !out) return fail(FL_ERR_INVALID, "null argument");
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
-  if (n != m->T * m->H) return fail(FL_ERR_INVALID, "size mismatch");
+  const Lane& L = lane0(m);
+  if (n != L.T * m->H) return fail(FL_ERR_INVALID, "size mismatch");
   int st;
   // fp32 copy, then (X tiled) the row-major fp16 rows just past it.
   void* tmp = workspace(m->ctx, (size_t)n * 4 + (m->x_tiled ? (size_t)n * m->esz : 0), &st);
   if (st) return st;
-  const void* x = m->X;
+  const void* x = L.X;
   if (m->x_tiled) {
     void* rm = (char*)tmp + (size_t)n * 4;
-    M_CHECK(launch_untile(m->dtype, m->X, m->T, m->H, rm, m->ctx->stream));
+    M_CHECK(launch_untile(m->dtype, L.X, L.T, m->H, rm, m->ctx->stream));
     x = rm;
   }
   M_CHECK(launch_cast(x, m->dtype, tmp, FL_F32, n, 0, m->ctx->stream));
