@@ -16,6 +16,8 @@
 // MFMA against a ones operand; with Q pre-scaled, the offset by the running
 // max rides in the score MFMA's accumulator, so the softmax costs one exp2,
 // half a max and half a pack per score.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -203,18 +205,24 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
   const u32x4_t ones = {AttnMfma<T>::kOnes, AttnMfma<T>::kOnes, AttnMfma<T>::kOnes,
                         AttnMfma<T>::kOnes};
 
+  // V^T fragment addresses in buffer 0, per 16-wide output tile dt; the
+  // buffer and the key-row step ride in the reads' immediate offsets.
+  uint32_t vaddr[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    vaddr[dt] = (uint32_t)(uintptr_t)(const lds_char*)lds[0][1] + vbase + (((dt * 2) ^ vx) << 4);
+
   const int ntiles = (L + BKV - 1) / BKV;
-  issue(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int cur = it & 1;
+  // One key tile; CUR (the LDS buffer holding it) is a compile-time
+  // constant, so every LDS address of the tile is a register plus an
+  // immediate.
+  auto tile = [&](int it, auto cur_c) __attribute__((always_inline)) {
+    constexpr int CUR = decltype(cur_c)::value;
     const int kv0 = it * BKV;
     // The other buffer was last read in the previous iteration, which
     // ended with a barrier.
-    if (it + 1 < ntiles) issue(kv0 + BKV, cur ^ 1);
-    const char* kt_lds = lds[cur][0];
-    const char* vt_lds = lds[cur][1];
+    if (it + 1 < ntiles) issue(kv0 + BKV, CUR ^ 1);
+    const char* kt_lds = lds[CUR][0];
 
     // Relative scores x, transposed: [key-tile][q-tile]
     float4_t s[4][2];
@@ -244,18 +252,17 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     // these reads from the DMA into the other buffer and would wait for it;
     // the s_waitcnt before the P V MFMAs covers their completion.
     u32x2_t vr[DT][4];  // [dt][ks*2 + half]
-    const uint32_t vb = (uint32_t)(uintptr_t)(const lds_char*)vt_lds + vbase;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t a = vb + (((dt * 2) ^ vx) << 4);
-      // Key rows +16, +32, +48 (the swizzle repeats every CH rows).
+      // Key rows +0, +16, +32, +48 (the swizzle repeats every CH rows).
       asm volatile(
-          "ds_read_b64_tr_b16 %0, %4\n"
-          "ds_read_b64_tr_b16 %1, %4 offset:%5\n"
-          "ds_read_b64_tr_b16 %2, %4 offset:%6\n"
-          "ds_read_b64_tr_b16 %3, %4 offset:%7\n"
+          "ds_read_b64_tr_b16 %0, %4 offset:%5\n"
+          "ds_read_b64_tr_b16 %1, %4 offset:%6\n"
+          "ds_read_b64_tr_b16 %2, %4 offset:%7\n"
+          "ds_read_b64_tr_b16 %3, %4 offset:%8\n"
           : "=&v"(vr[dt][0]), "=&v"(vr[dt][1]), "=&v"(vr[dt][2]), "=&v"(vr[dt][3])
-          : "v"(a), "n"(16 * ROWB), "n"(32 * ROWB), "n"(48 * ROWB));
+          : "v"(vaddr[dt]), "n"(CUR * 2 * TILE), "n"(CUR * 2 * TILE + 16 * ROWB),
+            "n"(CUR * 2 * TILE + 32 * ROWB), "n"(CUR * 2 * TILE + 48 * ROWB));
     }
     if (kv0 + BKV > L) {
 #pragma unroll
@@ -268,24 +275,30 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
           }
     }
 
-    // Row max; lazy rescale of the running output.  The first tile always
-    // sets m; later tiles move it only when a row max grows past 2^8.
-    float mx[2];
-    bool grow = it == 0;
+    // Lazy rescale of the running output.  The first tile always sets m;
+    // later tiles move it only when a row max grows past 2^8.  A row's
+    // scores sit in the four lanes {l, l^16, l^32, l^48}; one of them holds a
+    // score above the threshold iff the row max is above it, so the test
+    // takes this lane's max alone and the cross-lane reduction runs only
+    // when the wave rescales.
+    float lm = fmaxf(s[0][0][0], s[0][0][1]);
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float m = fmaxf(s[0][qt][0], s[0][qt][1]);
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-        for (int i = (kt == 0 ? 2 : 0); i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
-      mx[qt] = quad_max(m);
-      grow |= mx[qt] > kRescale;
-    }
-    if (__any(grow)) {
+        for (int i = 0; i < 4; ++i)
+          if (kt | qt | (i >> 1)) lm = fmaxf(lm, s[kt][qt][i]);
+    if (__any(it == 0 || lm > kRescale)) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float shift = it == 0 ? mx[qt] : fmaxf(mx[qt], 0.f);
+        float m = fmaxf(s[0][qt][0], s[0][qt][1]);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = (kt == 0 ? 2 : 0); i < 4; ++i) m = fmaxf(m, s[kt][qt][i]);
+        const float mx = quad_max(m);
+        const float shift = it == 0 ? mx : fmaxf(mx, 0.f);
         ms[qt] += shift;
         cinit[qt] = float4_t{-ms[qt], -ms[qt], -ms[qt], -ms[qt]};
 #pragma unroll
@@ -347,6 +360,14 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int it = 0; it < ntiles; it += 2) {
+    tile(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) tile(it + 1, std::integral_constant<int, 1>{});
   }
 
   T* out = (T*)p.out;

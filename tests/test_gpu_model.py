@@ -205,6 +205,31 @@ def test_config5_long_context_f16(ctx, fl, orc):
     assert c.min() >= COS_F16
 
 
+def test_sharp_attention_f16(ctx, fl, orc):
+    """Query and key projections scaled by 6: scores spread over tens of
+    units in the exp2 domain, so the attention kernel's running row max keeps
+    rising over key tiles and every rescale path (including the one applied
+    to scores already computed for the next tile from a Q pre-scaled in the
+    QKV epilogue) is exercised against the oracle."""
+    cfg = synth.nomic(layers=1)
+    w = dict(weights_for(cfg))
+    w["q_w.0"] = w["q_w.0"] * 6
+    w["k_w.0"] = w["k_w.0"] * 6
+    lengths = np.array([1000, 700, 129], np.int64)
+    ids = synth.make_ids(lengths)
+    m = fl.Model(ctx, cfg, dtype=fl.F16, math=fl.MATH_EXACT)
+    try:
+        m.load(w)
+        got = m.forward(ids, lengths)
+        assert m.status() == (False, False)
+    finally:
+        m.close()
+    want = orc.forward(cfg, w, ids, lengths)
+    c = cosines(got, want)
+    log(f"sharp attention min cos {c.min():.7f}")
+    assert c.min() >= COS_F16
+
+
 def test_bf16_model(ctx, fl, orc):
     cfg = synth.nomic(layers=2)
     lengths = np.array([256, 40], np.int64)

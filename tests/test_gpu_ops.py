@@ -376,6 +376,32 @@ def test_attention_flash_16bit(ctx, fl, orc, dtype, seq, hd):
     close(got, want, tol, tol)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("seq", [1000, 700])
+def test_attention_flash_growing_max(ctx, fl, dtype, seq):
+    """Keys grow with position, so row maxima rise tile after tile and the
+    kernel's running max and rescale of the partial output run in every
+    iteration, not only on the first key tile (16 and 11 key tiles)."""
+    dt = fl.F16 if dtype == "f16" else fl.BF16
+    heads, hd = 2, 64
+    rng = np.random.default_rng(seq)
+    q = rng.standard_normal((seq, heads * hd)).astype(np.float32)
+    k = (rng.standard_normal((seq, heads * hd)) *
+         (0.5 + np.arange(seq) / 150.0)[:, None]).astype(np.float32)
+    v = rng.standard_normal((seq, heads * hd)).astype(np.float32)
+    dq, dk, dv = ctx.tensor(q, dt), ctx.tensor(k, dt), ctx.tensor(v, dt)
+    qr, kr, vr = dq.numpy(), dk.numpy(), dv.numpy()
+    want = np.zeros_like(qr, dtype=np.float64)
+    for h in range(heads):
+        cs = slice(h * hd, (h + 1) * hd)
+        s = qr[:, cs].astype(np.float64) @ kr[:, cs].astype(np.float64).T * 0.125
+        p = np.exp(s - s.max(1, keepdims=True))
+        want[:, cs] = (p / p.sum(1, keepdims=True)) @ vr[:, cs]
+    got = ctx.attention(dq, dk, dv, 1, seq, heads, 0.125, fl.MATH_EXACT).numpy()
+    tol = 1e-2 if dt == fl.F16 else 6e-2
+    close(got, want, tol, tol)
+
+
 def test_attention_varlen_equals_per_sequence(ctx, fl, orc):
     lengths = [7, 64, 129, 1, 300]
     heads, hd = 2, 64
