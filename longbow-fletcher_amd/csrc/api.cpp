@@ -752,7 +752,7 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
                      [&](int a, int b) { return lengths[a] > lengths[b]; });
     for (int b : order)
       for (int h = 0; h < heads; ++h)
-        for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work.push_back(AttnWork{b, h, q0, 0});
+        for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work.push_back(AttnWork{cu[b], (int)lengths[b], h, q0});
   }
   const size_t cu_bytes = ((size_t)(nseq + 1) * 4 + 255) / 256 * 256;
   int st;

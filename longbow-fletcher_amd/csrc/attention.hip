@@ -120,8 +120,8 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 
   // The query blocks of one (sequence, head) run on one XCD and share its L2.
   const AttnWork w = p.work[xcd_group((int)blockIdx.x, (int)gridDim.x, p.group)];
-  const int s0 = p.cu[w.seq];
-  const int L = p.cu[w.seq + 1] - s0;
+  const int s0 = w.s0;
+  const int L = w.len;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, g = lane >> 4;
@@ -435,8 +435,8 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) float Vs[BKV * S];
 
   const AttnWork w = p.work[blockIdx.x];
-  const int s0 = p.cu[w.seq];
-  const int L = p.cu[w.seq + 1] - s0;
+  const int s0 = w.s0;
+  const int L = w.len;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lrow = lane & 15, lgrp = lane >> 4;
   const int hoff = w.head * D;

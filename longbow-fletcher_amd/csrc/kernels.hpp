@@ -147,11 +147,14 @@ hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, voi
 hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t stream);
 
 // ---- attention ------------------------------------------------------------
+// One query block of one (sequence, head).  The sequence's first row and
+// length ride in the item, so a workgroup needs a single dependent load
+// (its item) before it can address Q, K and V.
 struct AttnWork {
-  int seq;     // sequence index
+  int s0;      // first row of the sequence in the packed tensors
+  int len;     // sequence length
   int head;    // head index
   int q0;      // first query row (relative to the sequence start)
-  int pad;
 };
 // Flash attention (exact math, online softmax) for head_dim 32 or 64, 16-bit
 // types.  q_prescaled (head_dim 64 only): Q already holds q * scale * log2(e)

@@ -384,7 +384,7 @@ int prepare(fl_model* m, Lane& L, const int64_t* lengths, int nseq) {
                        [&](int a, int b) { return lengths[a] > lengths[b]; });
       for (int b : order)
         for (int h = 0; h < m->heads; ++h)
-          for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work[n_work++] = AttnWork{b, h, q0, 0};
+          for (int q0 = 0; q0 < (int)lengths[b]; q0 += bq) work[n_work++] = AttnWork{cu[b], (int)lengths[b], h, q0};
     }
     if (m->rope) {
       int st;
