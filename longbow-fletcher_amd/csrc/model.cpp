@@ -61,10 +61,15 @@ struct Staging {
 // Everything one batch's forward reads and writes besides the weights: the
 // activation buffers, the batch metadata and the stream the forward runs on.
 // Lane 0 runs on the context stream and serves every entry point; the
-// batching loop of fl_model_embed also uses lane 1 on a stream of its own, so
-// consecutive batches run concurrently and one batch's kernels fill the CUs
-// the other's leave idle (a 16384-token batch gives its N = 768 GEMMs 192
-// tiles for 256 CUs).
+// batching loop of fl_model_embed also uses lanes 1 .. kLanes-1, each on a
+// stream of its own, so consecutive batches run concurrently and one batch's
+// kernels fill the CUs the others' leave idle (a 16384-token batch gives its
+// N = 768 GEMMs 192 tiles for 256 CUs).  Three lanes (three of the four
+// hardware queues a process gets) measured best: two leave the device idle
+// while the host prepares the next batch, four gain nothing.
+// Lanes of fl_model_embed's batch pipeline (lane 0 is the context stream's).
+constexpr int kLanes = 3;
+
 struct Lane {
   hipStream_t stream = nullptr;
   // activations (capacity in tokens / sequences)
@@ -121,21 +126,21 @@ struct fl_model {
   float* pool_b = nullptr;
   std::unordered_map<void*, size_t> owned;  // device buffers and their sizes
 
-  // Lane 0: the context stream; lane 1: fl_model_embed's second stream.
-  Lane lane[2];
+  // Lane 0: the context stream; lanes 1 .. kLanes-1: fl_model_embed's own.
+  Lane lane[kLanes];
 
   // fl_model_embed's pipeline: ids go up on `up`, pooled vectors and the
   // batch's flags come back on `down`, forwards run on the lanes' streams.
   struct Pipe {
-    hipStream_t up = nullptr, down = nullptr;
-    int32_t* ids_pin[2] = {nullptr, nullptr};
-    float* out_pin[2] = {nullptr, nullptr};
-    int* flags_pin[2] = {nullptr, nullptr};
-    int* ids_dev[2] = {nullptr, nullptr};
-    float* out_dev[2] = {nullptr, nullptr};
-    uint16_t* out16_dev[2] = {nullptr, nullptr};  // fp16 output of the batch (FL_F16)
-    int* flags_dev[2] = {nullptr, nullptr};
-    hipEvent_t h2d[2] = {nullptr, nullptr}, fwd[2] = {nullptr, nullptr}, d2h[2] = {nullptr, nullptr};
+    int32_t* ids_pin[kLanes] = {};
+    float* out_pin[kLanes] = {};
+    int* flags_pin[kLanes] = {};
+    int* ids_dev[kLanes] = {};
+    float* out_dev[kLanes] = {};
+    uint16_t* out16_dev[kLanes] = {};  // fp16 output of the batch (FL_F16)
+    int* flags_dev[kLanes] = {};
+    hipEvent_t d2h[kLanes] = {};
+    bool ready = false;  // streams and events created
     int64_t cap_tok = 0;
     int cap_seq = 0;
   } pipe;
@@ -690,17 +695,17 @@ int fl_model_free(fl_model* m) {
     (void)activate(m->ctx);
     (void)hipStreamSynchronize(m->ctx->stream);
     fl_model::Pipe& P = m->pipe;
-    for (hipStream_t st : {P.up, P.down, m->lane[1].stream})
-      if (st) (void)hipStreamSynchronize(st);
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 1; k < kLanes; ++k)
+      if (m->lane[k].stream) (void)hipStreamSynchronize(m->lane[k].stream);
+    for (int k = 0; k < kLanes; ++k) {
       for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
         if (h) (void)hipHostFree(h);
-      for (hipEvent_t e : {P.h2d[k], P.fwd[k], P.d2h[k]})
-        if (e) (void)hipEventDestroy(e);
-      for (Lane& L : m->lane) free_staging(L.meta[k]);
+      if (P.d2h[k]) (void)hipEventDestroy(P.d2h[k]);
     }
-    for (hipStream_t st : {P.up, P.down, m->lane[1].stream})
-      if (st) (void)hipStreamDestroy(st);
+    for (Lane& L : m->lane)
+      for (Staging& sg : L.meta) free_staging(sg);
+    for (int k = 1; k < kLanes; ++k)
+      if (m->lane[k].stream) (void)hipStreamDestroy(m->lane[k].stream);
     free_owned(m);
     for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
   }
@@ -949,19 +954,19 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
   fl_model::Pipe& P = m->pipe;
   Lane& L0 = lane0(m);
   hipStream_t cs = m->ctx->stream;
-  if (!P.up) {
-    M_CHECK(hipStreamCreateWithFlags(&P.up, hipStreamNonBlocking));
-    M_CHECK(hipStreamCreateWithFlags(&P.down, hipStreamNonBlocking));
-    M_CHECK(hipStreamCreateWithFlags(&m->lane[1].stream, hipStreamNonBlocking));
-    for (int k = 0; k < 2; ++k)
-      for (hipEvent_t* e : {&P.h2d[k], &P.fwd[k], &P.d2h[k]})
-        M_CHECK(hipEventCreateWithFlags(e, hipEventDisableTiming));
+  if (!P.ready) {
+    for (int k = 1; k < kLanes; ++k)
+      if (!m->lane[k].stream)
+        M_CHECK(hipStreamCreateWithFlags(&m->lane[k].stream, hipStreamNonBlocking));
+    for (int k = 0; k < kLanes; ++k)
+      if (!P.d2h[k]) M_CHECK(hipEventCreateWithFlags(&P.d2h[k], hipEventDisableTiming));
+    P.ready = true;
   }
   if (max_bt > P.cap_tok || max_bs > P.cap_seq) {
-    for (hipStream_t st : {cs, P.up, P.down, m->lane[1].stream}) M_CHECK(hipStreamSynchronize(st));
+    for (int k = 0; k < kLanes; ++k) M_CHECK(hipStreamSynchronize(m->lane[k].stream));
     const int64_t ct = std::max(max_bt, P.cap_tok);
     const int cq = std::max(max_bs, P.cap_seq);
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < kLanes; ++k) {
       for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
         if (h) M_CHECK(hipHostFree(h));
       P.ids_pin[k] = nullptr;
@@ -972,10 +977,10 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
       untrack_free(m, P.out16_dev[k]);
       untrack_free(m, P.flags_dev[k]);
     }
-    // Capacities stay 0 until every buffer of both slots exists: a failure
+    // Capacities stay 0 until every buffer of every slot exists: a failure
     // here leaves null pointers and the next call reallocates.
     P.cap_tok = P.cap_seq = 0;
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < kLanes; ++k) {
       if (hipHostMalloc((void**)&P.ids_pin[k], (size_t)ct * 4, hipHostMallocDefault) != hipSuccess ||
           hipHostMalloc((void**)&P.out_pin[k], (size_t)cq * m->H * 4, hipHostMallocDefault) != hipSuccess ||
           hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess)
@@ -989,18 +994,19 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     P.cap_seq = cq;
   }
 
-  // Batch b uses slot and lane b & 1: consecutive batches compute on the two
-  // lanes' streams at the same time, each filling the CUs the other's
-  // kernels leave idle.  The host fills a slot's pinned ids only after that
-  // slot's previous batch has been copied back (so its upload and its
-  // forward are long done too), and copies results out of it at the same
-  // point: the host runs up to two batches ahead of the device, like the
-  // reference's double buffering of outputs (embeddings.go:766-775).
+  // Batch b uses slot and lane b % kLanes: consecutive batches compute on
+  // the lanes' streams at the same time, each filling the CUs the others'
+  // kernels leave idle.  A lane's stream carries its batch's upload, forward
+  // and download in order.  The host fills a slot's pinned ids only after
+  // that slot's previous batch has been copied back, and copies results out
+  // of it at the same point: the host runs up to kLanes batches ahead of the
+  // device, like the reference's double buffering of outputs
+  // (embeddings.go:766-775) with one more buffer.
   const int64_t H = m->H;
   const size_t osz = out_dtype == FL_F16 ? 2 : 4;
   auto drain = [&](int b) -> int {
     const Batch& pb = plan[(size_t)b];
-    const int k = b & 1;
+    const int k = b % kLanes;
     M_CHECK(hipEventSynchronize(P.d2h[k]));
     std::memcpy((char*)out + (size_t)pb.first * H * osz, P.out_pin[k], (size_t)pb.count * H * osz);
     if (batch_nan)
@@ -1010,13 +1016,12 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
   const int nb = (int)plan.size();
   for (int b = 0; b < nb; ++b) {
     const Batch& pb = plan[(size_t)b];
-    const int k = b & 1;
-    if (b >= 2) M_ST(drain(b - 2));
+    const int k = b % kLanes;
+    if (b >= kLanes) M_ST(drain(b - kLanes));
     for (int64_t t = 0; t < pb.tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[pb.tok0 + t];
-    M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)pb.tokens * 4, hipMemcpyHostToDevice, P.up));
-    M_CHECK(hipEventRecord(P.h2d[k], P.up));
     Lane& L = m->lane[k];
-    M_CHECK(hipStreamWaitEvent(L.stream, P.h2d[k], 0));
+    M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)pb.tokens * 4, hipMemcpyHostToDevice,
+                           L.stream));
     M_ST(prepare(m, L, lengths + pb.first, pb.count));
     M_ST(run(m, L, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
     const void* dev_out = P.out_dev[k];
@@ -1025,15 +1030,14 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
                           L.stream));
       dev_out = P.out16_dev[k];
     }
-    M_CHECK(hipEventRecord(P.fwd[k], L.stream));
-    M_CHECK(hipStreamWaitEvent(P.down, P.fwd[k], 0));
-    M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)pb.count * H * osz, hipMemcpyDeviceToHost, P.down));
-    M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, P.down));
-    M_CHECK(hipEventRecord(P.d2h[k], P.down));
+    M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)pb.count * H * osz, hipMemcpyDeviceToHost,
+                           L.stream));
+    M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, L.stream));
+    M_CHECK(hipEventRecord(P.d2h[k], L.stream));
   }
-  for (int b = std::max(0, nb - 2); b < nb; ++b) M_ST(drain(b));
+  for (int b = std::max(0, nb - kLanes); b < nb; ++b) M_ST(drain(b));
   // fl_model_status then reports the last batch (drained, so its forward is done).
-  M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[(nb - 1) & 1], 8, hipMemcpyDeviceToDevice, cs));
+  M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[(nb - 1) % kLanes], 8, hipMemcpyDeviceToDevice, cs));
   if (nbatches) *nbatches = nb;
   return FL_OK;
 }
