@@ -291,9 +291,10 @@ int fl_model_forward_device(fl_model *model, const int32_t *d_ids, const int64_t
  * sequences are taken in order into batches that end before the sequence
  * that would pass max_seqs sequences or max_tokens tokens (a batch always
  * holds at least one; the reference's Linux GPU defaults are 512 and 16384,
- * embeddings.go:84-131), and each batch runs the model forward.  Ids go up
- * and pooled vectors come back on copy streams while the next batch
- * computes, replacing the reference's double-buffered outputs (:766-775).
+ * embeddings.go:84-131), and each batch runs the model forward.  Consecutive
+ * batches run on three streams at once, each carrying its batch's id upload,
+ * forward and vector download, replacing the reference's double-buffered
+ * outputs (:766-775).
  * ids: flat host ids of all sequences (framing included, as in
  * fl_model_forward); out: host fp32 [nseq x hidden] in input order;
  * batch_nan (optional) int32 [nseq]: 1 where the sequence's batch output held
