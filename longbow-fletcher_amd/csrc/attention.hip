@@ -245,25 +245,6 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) s[kt][qt][i] = fmaf(s[kt][qt][i], c, -ms[qt]);
     }
-    // V^T fragments of this tile, read while the softmax runs, with the
-    // transposing LDS load ds_read_b64_tr_b16: within each 16-lane block,
-    // lane i receives element i%4 of the 8-byte rows addressed by lanes
-    // i/4 + 4j, j = 0..3.  Written as asm because the compiler cannot tell
-    // these reads from the DMA into the other buffer and would wait for it;
-    // the s_waitcnt before the P V MFMAs covers their completion.
-    u32x2_t vr[DT][4];  // [dt][ks*2 + half]
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      // Key rows +0, +16, +32, +48 (the swizzle repeats every CH rows).
-      asm volatile(
-          "ds_read_b64_tr_b16 %0, %4 offset:%5\n"
-          "ds_read_b64_tr_b16 %1, %4 offset:%6\n"
-          "ds_read_b64_tr_b16 %2, %4 offset:%7\n"
-          "ds_read_b64_tr_b16 %3, %4 offset:%8\n"
-          : "=&v"(vr[dt][0]), "=&v"(vr[dt][1]), "=&v"(vr[dt][2]), "=&v"(vr[dt][3])
-          : "v"(vaddr[dt]), "n"(CUR * 2 * TILE), "n"(CUR * 2 * TILE + 16 * ROWB),
-            "n"(CUR * 2 * TILE + 32 * ROWB), "n"(CUR * 2 * TILE + 48 * ROWB));
-    }
     if (kv0 + BKV > L) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -331,30 +312,42 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
       }
     }
 
-    // O^T += V^T P^T; the row sums ride along as ones * P^T.
-    {
+    // O^T += V^T P^T; the row sums ride along as ones * P^T.  V^T
+    // fragments come from the transposing LDS load ds_read_b64_tr_b16
+    // (within each 16-lane block, lane i receives element i%4 of the 8-byte
+    // rows addressed by lanes i/4 + 4j, j = 0..3), one 32-key step at a
+    // time after the softmax: read earlier, they would be live beside the
+    // scores and take the kernel past 128 VGPRs, from four waves per SIMD
+    // to three.  Written as asm because the compiler cannot tell these
+    // reads from the DMA into the other buffer and would wait for it.
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x2_t vr[DT][2];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %2 offset:%3\n"
+            "ds_read_b64_tr_b16 %1, %2 offset:%4\n"
+            : "=&v"(vr[dt][0]), "=&v"(vr[dt][1])
+            : "v"(vaddr[dt]), "n"(CUR * 2 * TILE + ks * 32 * ROWB),
+              "n"(CUR * 2 * TILE + (ks * 32 + 16) * ROWB));
+      }
+      AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
+      AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
       if constexpr (DT == 4) {
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
-                       "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]),
-                       "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[2][2]), "+v"(vr[2][3]),
-                       "+v"(vr[3][0]), "+v"(vr[3][1]), "+v"(vr[3][2]), "+v"(vr[3][3]));
+                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[1][0]), "+v"(vr[1][1]),
+                       "+v"(vr[2][0]), "+v"(vr[2][1]), "+v"(vr[3][0]), "+v"(vr[3][1]));
       } else {
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[0][2]), "+v"(vr[0][3]),
-                       "+v"(vr[1][0]), "+v"(vr[1][1]), "+v"(vr[1][2]), "+v"(vr[1][3]));
+                     : "+v"(vr[0][0]), "+v"(vr[0][1]), "+v"(vr[1][0]), "+v"(vr[1][1]));
       }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        AttnMfma<T>::mma(lacc[0], ones, pf[ks][0]);
-        AttnMfma<T>::mma(lacc[1], ones, pf[ks][1]);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const u32x2_t lo = vr[dt][ks * 2], hi = vr[dt][ks * 2 + 1];
-          const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
-          AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
-          AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
-        }
+      for (int dt = 0; dt < DT; ++dt) {
+        const u32x2_t lo = vr[dt][0], hi = vr[dt][1];
+        const u32x4_t vf = {lo[0], lo[1], hi[0], hi[1]};
+        AttnMfma<T>::mma(o[dt][0], vf, pf[ks][0]);
+        AttnMfma<T>::mma(o[dt][1], vf, pf[ks][1]);
       }
     }
 
