@@ -336,6 +336,8 @@ def main():
             for first, count in plan:
                 model.forward(ids[starts[first]:starts[first + count]], lengths[first:first + count])
         seq_s = (time.perf_counter() - t0) / reps
+        # Untimed first call: the fp16 cast kernel's first launch loads it.
+        model.embed(ids, lengths, ms_, mt_, out_dtype=fl.F16)
         t0 = time.perf_counter()
         for _ in range(reps):
             model.embed(ids, lengths, ms_, mt_, out_dtype=fl.F16)
