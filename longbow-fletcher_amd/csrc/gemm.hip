@@ -17,31 +17,21 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
-// Ping-pong kernel (16-bit GEMMs with N % 256 == 0): K step, LDS stages and
-// row-block group of the tile order.
-#ifndef FL_GEMM_PP
-#define FL_GEMM_PP 1
-#endif
-#ifndef FL_GEMM_PP_BK
-#define FL_GEMM_PP_BK 32
-#endif
-#ifndef FL_GEMM_PP_NS
-#define FL_GEMM_PP_NS 4
-#endif
-#ifndef FL_GEMM_PP_SPREAD
-#define FL_GEMM_PP_SPREAD 8
-#endif
-#ifndef FL_GEMM_W4
-#define FL_GEMM_W4 1
-#endif
-#ifndef FL_GEMM_FUSE
-#define FL_GEMM_FUSE 1
-#endif
-#ifndef FL_GEMM_PP_GROUP_M
-#define FL_GEMM_PP_GROUP_M 8
-#endif
-
 namespace fl {
+
+// Tuning constants, chosen by measurement on MI355X.
+// Ping-pong kernel (16-bit, N % 256 == 0, the layouts the four-wave kernel
+// does not take): K step, LDS stages, and the SwiGLU output staging (KB per
+// wave) that sets how many row blocks are stored per compute tick.
+constexpr int kPpBK = 32, kPpNS = 4, kPpSpread = 8;
+// Row blocks per group of the persistent tile order (an XCD's workgroups
+// share a group's activation rows in L2).
+constexpr int kGroupM = 8;
+// Four-wave kernel: the next tile's first K step runs inside the epilogue.
+constexpr bool kW4Fuse = true;
+// Direct-LDS 16-bit GEMM (plain layouts): K step, LDS stages (48 KB, two
+// workgroups per CU) and chunk swizzle (row >> 1) & 3.
+constexpr int kLdsBK = 32, kLdsStages = 2, kLdsSwz = 1;
 
 // Register-level K steps and accumulator reads of gemm_w4_kernel.
 #include "gemm_w4.inc"
@@ -725,13 +715,13 @@ __global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) 
   constexpr int KS = BK / 32;                  // MFMA k steps per K step
   constexpr int TM = 8, FN = 4, WTM = 128, WTN = 64;
   constexpr int NLD = STAGE / 1024 / 8;        // 1 KB DMA loads per wave per step
-  constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
+  constexpr int GROUP_M = kGroupM;
   static_assert(BK == 32 || BK == 64, "BK 32 or 64");
   // SwiGLU stages NSTG of each wave's 8 finished row blocks in LDS (1 KB
   // each) and stores them over the following compute ticks.  (Staging half
   // of the plain STORE epilogue's rows, at the cost of a stage, was slower.)
   constexpr bool STAGE_OUT = EPI == EPI_SWIGLU;
-  constexpr int NSTG = FL_GEMM_PP_SPREAD;
+  constexpr int NSTG = kPpSpread;
   constexpr int OUTW = STAGE_OUT ? NSTG * 1024 : 0;
   static_assert(NS >= 2 && NS * STAGE + 8 * OUTW <= 160 * 1024, "LDS stages");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 8 * OUTW];
@@ -1063,7 +1053,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   constexpr int BM = 256, BN = 256, BK = 32, ROWB = 64;
   constexpr int STAGE = (BM + BN) * ROWB;     // 32 KB
   constexpr int NLD = 8;                      // 1 KB loads per wave per step
-  constexpr int GROUP_M = FL_GEMM_PP_GROUP_M;
+  constexpr int GROUP_M = kGroupM;
   constexpr bool F16T = Elem<T>::dtype == F16;
   static_assert(NS == 4, "the K loop runs in groups of four steps, one per stage");
   // NS stages, then an 8 KB epilogue staging area per wave.
@@ -1202,7 +1192,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // accumulator reads of the tile it restarts, so the MFMAs execute while the
   // reads and the epilogue's math issue.  fused_read(t, h, v) returns the
   // accumulators of row block t, feature group h (v[f] = tile 8(4h+f) + t).
-  constexpr bool FUSE = FL_GEMM_FUSE && EPI != EPI_ROPE;
+  constexpr bool FUSE = kW4Fuse && EPI != EPI_ROPE;
   auto fused_read = [&](auto tc, auto hc, float4_t (&v)[4]) __attribute__((always_inline)) {
     constexpr int TB = decltype(tc)::value, HB = decltype(hc)::value;
     constexpr uint32_t RD1 = (1 % NS) * STAGE;
@@ -1469,17 +1459,6 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 // tiles of 4 waves x (128x64); fp32 128x64 tiles of 2 waves.
 // ---------------------------------------------------------------------------
 struct Cfg256x128 { static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2; };
-// Direct-LDS 16-bit GEMM defaults: 256x128 tiles, BK = 32, two LDS stages
-// (48 KB, so two workgroups share a CU), chunk swizzle (row >> 1) & 3.
-#ifndef FL_GEMM_SWZ
-#define FL_GEMM_SWZ 1
-#endif
-#ifndef FL_GEMM_STAGES
-#define FL_GEMM_STAGES 2
-#endif
-#ifndef FL_GEMM_BK
-#define FL_GEMM_BK 32
-#endif
 struct CfgF32 { static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1; };
 
 template <typename T, typename C, int EPI, int MATH>
@@ -1488,8 +1467,8 @@ static hipError_t launch_lds(const GemmParams& p, hipStream_t s) {
   const int num_n = p.N / C::BN;
   dim3 grid(num_m * num_n), block(C::WM * C::WN * 64);
   hipLaunchKernelGGL(
-      (gemm_lds_kernel<T, C::BM, C::BN, FL_GEMM_BK, C::WM, C::WN, EPI, MATH, FL_GEMM_SWZ,
-                       FL_GEMM_STAGES>),
+      (gemm_lds_kernel<T, C::BM, C::BN, kLdsBK, C::WM, C::WN, EPI, MATH, kLdsSwz,
+                       kLdsStages>),
       grid, block, 0, s, p);
   return hipGetLastError();
 }
@@ -1534,10 +1513,10 @@ template <typename T, int EPI, int MATH>
 static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
   const int grid = persistent_grid(ntiles);
-  // SwiGLU's output staging area (8 waves x FL_GEMM_PP_SPREAD KB) takes the
+  // SwiGLU's output staging area (8 waves x kPpSpread KB) takes the
   // LDS of one stage when it exceeds the 32 KB that four stages leave.
-  constexpr int NS = EPI == EPI_SWIGLU && FL_GEMM_PP_SPREAD > 4 ? FL_GEMM_PP_NS - 1 : FL_GEMM_PP_NS;
-  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, FL_GEMM_PP_BK, NS>), dim3(grid), dim3(512), 0,
+  constexpr int NS = EPI == EPI_SWIGLU && kPpSpread > 4 ? kPpNS - 1 : kPpNS;
+  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, kPpBK, NS>), dim3(grid), dim3(512), 0,
                      s, p, ntiles);
   return hipGetLastError();
 }
@@ -1545,7 +1524,7 @@ static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
 // The four-wave kernel's K loop runs in groups of four steps with at least
 // two groups per tile; its RoPE epilogue gives both 64-feature heads of a
 // wave the same table and rotation.
-static bool gemm_w4_shape_ok(int K) { return FL_GEMM_W4 && K % 128 == 0 && K >= 256; }
+static bool gemm_w4_shape_ok(int K) { return K % 128 == 0 && K >= 256; }
 static bool gemm_w4_ok(const GemmParams& p) {
   if (!gemm_w4_shape_ok(p.K)) return false;
   if (p.epi.kind == EPI_ROPE && (p.epi.q_cols % 128 || p.epi.rope_cols % 128)) return false;
@@ -1586,7 +1565,7 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
       }
       return hipErrorInvalidValue;
     }
-    if (p.K % (FL_GEMM_BK * FL_GEMM_STAGES) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
+    if (p.K % (kLdsBK * kLdsStages) == 0) return launch_lds<T, Cfg256x128, EPI, MATH>(p, s);
     return launch_cfg<T, Cfg256x128, EPI, MATH>(p, s);
   }
 }
@@ -1617,11 +1596,11 @@ static bool cfg_ok(int N, int K) {
 }
 
 int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
-  if (!FL_GEMM_PP || (dtype != F16 && dtype != BF16)) return -1;
-  if (N <= 0 || K <= 0 || N % 256 || K % FL_GEMM_PP_BK) return -1;
+  if (dtype != F16 && dtype != BF16) return -1;
+  if (N <= 0 || K <= 0 || N % 256 || K % kPpBK) return -1;
   if (!pp_epilogue_ok(epi_kind, math)) return -1;
   // SwiGLU stores a tile's staged row blocks over the next tile's K steps.
-  if (epi_kind == EPI_SWIGLU && K / FL_GEMM_PP_BK < 8) return -1;
+  if (epi_kind == EPI_SWIGLU && K / kPpBK < 8) return -1;
   if (epi_kind == EPI_ROPE) return has_bias ? -1 : PACK_ROPE;
   return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
 }

@@ -24,9 +24,6 @@
 #include "context.hpp"
 #include "kernels.hpp"
 
-#ifndef FL_FFN_TILED
-#define FL_FFN_TILED 1
-#endif
 
 namespace fl {
 
@@ -631,7 +628,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     // ping-pong kernel, whose epilogue applies the scale.
     m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
                      m->H % 64 == 0;
-    m->ffn_tiled = FL_FFN_TILED && m->swiglu && m->lay_up == PACK_SWIGLU_LANE && m->lay_down >= PACK_LANE16 &&
+    m->ffn_tiled = m->swiglu && m->lay_up == PACK_SWIGLU_LANE && m->lay_down >= PACK_LANE16 &&
                    gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, false,
                                  false) &&
                    gemm_tiled_ok(m->dtype, m->H, m->I, EPI_STORE, c.math, has_bias, false, true,
