@@ -166,6 +166,42 @@ __global__ void rope_kernel(T* t, int rows, int heads, int hd, int ld, const int
   }
 }
 
+// The same for 16-bit tensors with 16-byte aligned rows and half % 8 == 0:
+// one work item = 8 consecutive pairs (j, j + half) of one head of one row,
+// two 16-byte loads and stores of the tensor and four of the table, with
+// the arithmetic of rope_kernel.
+template <typename T>
+__global__ void __launch_bounds__(256)
+rope_vec_kernel(T* t, int rows, int heads, int hd, int ld, const int* pos, const float2* cs) {
+#pragma clang fp contract(off)
+  using V8 = T __attribute__((ext_vector_type(8)));
+  const int half = hd / 2, cph = half / 8;  // 8-pair chunks per head
+  const int per_row = heads * cph;
+  const int64_t total = (int64_t)rows * per_row;
+  FL_GRID_STRIDE(i, total) {
+    const int r = (int)(i / per_row);
+    const int rem = (int)(i - (int64_t)r * per_row);
+    const int h = rem / cph, j0 = (rem - h * cph) * 8;
+    T* x = t + (size_t)r * ld + h * hd + j0;
+    const float4_t* c4 = (const float4_t*)(cs + (size_t)pos[r] * half + j0);
+    const V8 a = *(const V8*)x, b = *(const V8*)(x + half);
+    V8 oa, ob;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4_t c = c4[q];  // (cos, sin) of pairs j0 + 2q, j0 + 2q + 1
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float x1 = to_f(a[2 * q + e]), x2 = to_f(b[2 * q + e]);
+        const float co = c[2 * e], si = c[2 * e + 1];
+        oa[2 * q + e] = from_f<T>(x1 * co - x2 * si);
+        ob[2 * q + e] = from_f<T>(x1 * si + x2 * co);
+      }
+    }
+    *(V8*)x = oa;
+    *(V8*)(x + half) = ob;
+  }
+}
+
 // Masked mean-pool, stage 1: per (sequence, row chunk) column sums into
 // part[seq][chunk][cols] (deterministic, no atomics).
 template <typename T>
@@ -418,6 +454,17 @@ hipError_t launch_rope(int dtype, void* t, int rows, int heads, int head_dim, in
                        const int* pos, const float2* cs, hipStream_t s) {
   const int64_t total = (int64_t)rows * heads * (head_dim / 2);
   if (total <= 0) return hipSuccess;
+  if (dtype != F32 && (head_dim / 2) % 8 == 0 && ld % 8 == 0 && ((uintptr_t)t & 15) == 0 &&
+      (int64_t)rows * heads * (head_dim / 16) < INT64_C(1) << 31) {
+    const int64_t items = total / 8;
+    if (dtype == F16)
+      hipLaunchKernelGGL(rope_vec_kernel<_Float16>, grid_for(items, 256 * 2), dim3(256), 0, s,
+                         (_Float16*)t, rows, heads, head_dim, ld, pos, cs);
+    else
+      hipLaunchKernelGGL(rope_vec_kernel<__bf16>, grid_for(items, 256 * 2), dim3(256), 0, s,
+                         (__bf16*)t, rows, heads, head_dim, ld, pos, cs);
+    return hipGetLastError();
+  }
   FL_DISPATCH(dtype, T, hipLaunchKernelGGL(rope_kernel<T>, grid_for(total), dim3(256), 0, s,
                                            (T*)t, rows, heads, head_dim, ld, pos, cs));
   return hipGetLastError();
