@@ -112,6 +112,13 @@ int fl_get_stream(fl_context *ctx, void **stream);
 /* Cuda_Alloc (cuda_bridge.h:23).  The buffer is zero-filled, as
  * Backend.GetTensor requires (cpu_backend.go:147-156, device_test.go:98-112). */
 int fl_alloc(fl_context *ctx, int64_t bytes, void **out);
+/* fl_alloc without the zero fill, for the result tensors of the producing
+ * ops (Linear, LinearActivation, Attention, Gather, Cast, Slice, and
+ * NewTensor with data: device.go:5-117), which write them whole.  The
+ * reference's Metal backend zero-fills those too (NewTensorWithType,
+ * metal_darwin.go:100-125); this skips one write pass over every result.
+ * Contents are undefined until written. */
+int fl_alloc_uninit(fl_context *ctx, int64_t bytes, void **out);
 /* Cuda_FreeBuffer (cuda_bridge.h:24); Backend.PutTensor (device.go:146).  The
  * buffer goes back to the context's cache without waiting for the device
  * (like the Metal pool, metal_darwin.go:151-274): a later fl_alloc may hand

@@ -70,6 +70,7 @@ _SIGS = {
     "fl_vram_usage": ([_vp, C.POINTER(_i64), C.POINTER(_i64)], _i),
     "fl_get_stream": ([_vp, C.POINTER(_vp)], _i),
     "fl_alloc": ([_vp, _i64, C.POINTER(_vp)], _i),
+    "fl_alloc_uninit": ([_vp, _i64, C.POINTER(_vp)], _i),
     "fl_free": ([_vp, _vp], _i),
     "fl_pool_stats": ([_vp, C.POINTER(_i64)], _i),
     "fl_pool_trim": ([_vp], _i),
@@ -249,16 +250,24 @@ class Context:
         check(lib().fl_alloc(self.h, n * _ESZ[dtype], C.byref(p)))
         return DeviceArray(self, p.value, shape, dtype)
 
+    def result(self, shape, dtype: int = F32) -> DeviceArray:
+        """The result tensor of a producing op, which writes it whole: not
+        zero-filled (fl_alloc_uninit)."""
+        n = int(np.prod(shape)) if len(shape) else 1
+        p = C.c_void_p()
+        check(lib().fl_alloc_uninit(self.h, n * _ESZ[dtype], C.byref(p)))
+        return DeviceArray(self, p.value, shape, dtype)
+
     def tensor(self, data, dtype: int = F32, rounding: int = ROUND_NEAREST) -> DeviceArray:
         """Backend.NewTensorWithType + CopyFromFloat32."""
         a = np.ascontiguousarray(data, dtype=np.float32)
-        t = self.empty(a.shape, dtype)
+        t = self.result(a.shape, dtype)
         check(lib().fl_upload_f32(self.h, t.ptr, dtype, a.ctypes.data, a.size, rounding))
         return t
 
     def int32(self, data) -> DeviceArray:
         a = np.ascontiguousarray(data, dtype=np.int32)
-        t = self.empty(a.shape, F32)
+        t = self.result(a.shape, F32)
         check(lib().fl_copy_to_device(self.h, t.ptr, a.ctypes.data, a.nbytes))
         return t
 
@@ -267,7 +276,7 @@ class Context:
         m = a.shape[1] if trans_a else a.shape[0]
         k = a.shape[0] if trans_a else a.shape[1]
         n = b.shape[0] if trans_b else b.shape[1]
-        c = self.empty((m, n), a.dtype)
+        c = self.result((m, n), a.dtype)
         check(lib().fl_gemm(self.h, a.dtype, int(trans_a), int(trans_b), m, n, k, alpha, a.ptr,
                             a.shape[1], b.ptr, b.shape[1], c.ptr, n))
         return c
@@ -276,7 +285,7 @@ class Context:
                math=MATH_REFERENCE, w_layout=W_IN_OUT):
         rows, k = x.shape
         n = w.shape[1] if w_layout == W_IN_OUT else w.shape[0]
-        out = self.empty((rows, n // 2 if act == ACT_SWIGLU else n), x.dtype)
+        out = self.result((rows, n // 2 if act == ACT_SWIGLU else n), x.dtype)
         check(lib().fl_linear(self.h, x.dtype, x.ptr, rows, k, w.ptr, w_layout, n, _ptr(bias),
                               act, math, out.ptr))
         return out
@@ -306,7 +315,7 @@ class Context:
 
     def gather(self, table: DeviceArray, idx) -> DeviceArray:
         idx = np.ascontiguousarray(idx, np.int64)
-        out = self.empty((idx.size, table.shape[1]), table.dtype)
+        out = self.result((idx.size, table.shape[1]), table.dtype)
         check(lib().fl_gather_rows(self.h, table.dtype, table.ptr, table.shape[0],
                                    table.shape[1], idx.ctypes.data, idx.size, out.ptr))
         return out
@@ -320,21 +329,21 @@ class Context:
                                    heads, head_dim, base))
 
     def attention(self, q, k, v, batch, seq, heads, scale, math=MATH_REFERENCE):
-        out = self.empty(q.shape, q.dtype)
+        out = self.result(q.shape, q.dtype)
         check(lib().fl_attention(self.h, q.dtype, q.ptr, k.ptr, v.ptr, out.ptr, batch, seq, heads,
                                  q.shape[1], scale, math))
         return out
 
     def attention_varlen(self, q, k, v, lengths, heads, scale, math=MATH_REFERENCE):
         lengths = np.ascontiguousarray(lengths, np.int64)
-        out = self.empty(q.shape, q.dtype)
+        out = self.result(q.shape, q.dtype)
         check(lib().fl_attention_varlen(self.h, q.dtype, q.ptr, k.ptr, v.ptr, out.ptr,
                                         lengths.ctypes.data, lengths.size, heads, q.shape[1],
                                         scale, math))
         return out
 
     def cast(self, t: DeviceArray, dtype: int) -> DeviceArray:
-        out = self.empty(t.shape, dtype)
+        out = self.result(t.shape, dtype)
         check(lib().fl_cast(self.h, t.ptr, t.dtype, out.ptr, dtype, t.size))
         return out
 
@@ -344,7 +353,7 @@ class Context:
         return bool(r.value)
 
     def slice(self, t: DeviceArray, r0, r1, c0, c1) -> DeviceArray:
-        out = self.empty((max(r1 - r0, 0), max(c1 - c0, 0)), t.dtype)
+        out = self.result((max(r1 - r0, 0), max(c1 - c0, 0)), t.dtype)
         check(lib().fl_slice(self.h, t.dtype, t.ptr, t.shape[0], t.shape[1], r0, r1, c0, c1,
                              out.ptr))
         return out
@@ -356,7 +365,7 @@ class Context:
         then be given)."""
         lengths = np.ascontiguousarray(lengths, np.int64)
         if out is None:
-            out = self.empty((lengths.size, hidden.shape[1]), F32)
+            out = self.result((lengths.size, hidden.shape[1]), F32)
         f = lib().fl_mean_pool_noalloc if noalloc else lib().fl_mean_pool
         check(f(self.h, hidden.dtype, hidden.ptr, hidden.shape[1], lengths.ctypes.data,
                 lengths.size, int(l2), out.ptr))

@@ -299,23 +299,34 @@ int fl_get_stream(fl_context* ctx, void** stream) {
   return FL_OK;
 }
 
-int fl_alloc(fl_context* ctx, int64_t bytes, void** out) {
-  FL_ENTER(ctx);
+static int alloc_block(fl_context* ctx, int64_t bytes, bool zero, void** out) {
   if (!out || bytes < 0) return fail(FL_ERR_INVALID, "bad allocation request");
   *out = nullptr;
   void* p = nullptr;
   size_t cls = 0;
   if (int st = pool_get(ctx, bytes > 0 ? (size_t)bytes : 16, &p, &cls)) return st;
-  // Backend.GetTensor hands out zeroed memory (cpu_backend.go:147-156); the
-  // fill is ordered on the stream after any earlier use of a reused block.
-  hipError_t e = hipMemsetAsync(p, 0, bytes > 0 ? (size_t)bytes : 16, ctx->stream);
-  if (e != hipSuccess) {
-    pool_put(ctx, p, cls, ctx->device);
-    return hip_fail(e, "hipMemsetAsync");
+  if (zero) {
+    // Backend.GetTensor hands out zeroed memory (cpu_backend.go:147-156); the
+    // fill is ordered on the stream after any earlier use of a reused block.
+    hipError_t e = hipMemsetAsync(p, 0, bytes > 0 ? (size_t)bytes : 16, ctx->stream);
+    if (e != hipSuccess) {
+      pool_put(ctx, p, cls, ctx->device);
+      return hip_fail(e, "hipMemsetAsync");
+    }
   }
   ctx->live[(uintptr_t)p] = fl_context::Live{cls, ctx->device, ++ctx->gen_counter};
   *out = p;
   return FL_OK;
+}
+
+int fl_alloc(fl_context* ctx, int64_t bytes, void** out) {
+  FL_ENTER(ctx);
+  return alloc_block(ctx, bytes, true, out);
+}
+
+int fl_alloc_uninit(fl_context* ctx, int64_t bytes, void** out) {
+  FL_ENTER(ctx);
+  return alloc_block(ctx, bytes, false, out);
 }
 
 int fl_free(fl_context* ctx, void* ptr) {

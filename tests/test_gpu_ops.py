@@ -66,6 +66,44 @@ def test_get_tensor_zeroed(ctx, fl):
     assert float(np.abs(t2.numpy()).max()) == 0.0
 
 
+def test_results_written_whole_on_recycled_blocks(ctx, fl):
+    # The producing ops' results come from fl_alloc_uninit: each test below
+    # first frees a block of the result's size class filled with NaN bytes
+    # (fl_memset 0xFF), so the result reuses poisoned memory, then checks the
+    # whole result against a zero-filled run of the same op.
+    import ctypes
+
+    def poison(shape, dtype):
+        t = ctx.empty(shape, dtype)
+        fl.check(fl.lib().fl_memset(ctx.h, ctypes.c_void_p(t.ptr), 0xFF, t.nbytes))
+        t.free()
+
+    x16 = ctx.tensor(rand(300, 256), fl.F16)
+    w16 = ctx.tensor(rand(256, 512, scale=0.05), fl.F16)
+    b16 = ctx.tensor(rand(1, 512), fl.F16)
+    q, k, v = (ctx.tensor(rand(256, 128), fl.F16) for _ in range(3))
+    cases = {
+        "linear": ((300, 512), fl.F16, lambda: ctx.linear(x16, w16, b16, math=fl.MATH_EXACT)),
+        "swiglu": ((300, 256), fl.F16,
+                   lambda: ctx.linear(x16, w16, b16, act=fl.ACT_SWIGLU, math=fl.MATH_EXACT)),
+        "gemm": ((300, 512), fl.F16, lambda: ctx.gemm(x16, w16)),
+        "attention": ((256, 128), fl.F16,
+                      lambda: ctx.attention(q, k, v, 2, 128, 2, 0.125, math=fl.MATH_EXACT)),
+        "gather": ((5, 256), fl.F16, lambda: ctx.gather(x16, np.array([4, 0, 299, 7, 7]))),
+        "cast": ((300, 256), fl.F32, lambda: ctx.cast(x16, fl.F32)),
+        "slice": ((100, 64), fl.F16, lambda: ctx.slice(x16, 10, 110, 32, 96)),
+        "mean_pool": ((2, 256), fl.F32, lambda: ctx.mean_pool(x16, np.array([100, 200]))),
+        "upload": ((300, 256), fl.F16, lambda: ctx.tensor(rand(300, 256), fl.F16)),
+    }
+    for name, (shape, dtype, op) in cases.items():
+        poison(shape, dtype)
+        got = op()
+        vals = got.numpy()
+        assert vals.shape == shape, name
+        assert np.isfinite(vals).all(), f"{name}: result not written whole"
+        got.free()
+
+
 def test_known_cast(ctx, fl):
     # cast_test.go:11-47: 1.0 -> 0x3c00, -2.0 -> 0xc000
     t = ctx.tensor(np.array([[1.0, -2.0]], np.float32))
