@@ -1605,6 +1605,13 @@ int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bia
   return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
 }
 
+int gemm_padded_width(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
+  if (N <= 0 || N % 256 == 0 || epi_kind == EPI_SWIGLU || epi_kind == EPI_ROPE) return N;
+  const int np = (N + 255) / 256 * 256;
+  return gemm_pp_layout(dtype, np, K, epi_kind, math, has_bias) >= 0 && gemm_w4_shape_ok(K) ? np
+                                                                                           : N;
+}
+
 bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
                    bool a_tiled, bool c_padded) {
   if (!out_tiled && !a_tiled && !c_padded) return true;
@@ -1733,9 +1740,12 @@ hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N
 // ---------------------------------------------------------------------------
 // Weight packing: out[n][k] = in[k][n]; with SwiGLU interleave the [gate|up]
 // output columns are reordered into 16-column blocks g0 u0 g1 u1 ...
+// Column n of the input becomes row row0 + n of a packed matrix of ntot rows
+// (one part of a fused QKV matrix, or a matrix with zero padding rows).
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int layout) {
+__global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int layout, int row0,
+                                 int ntot) {
   __shared__ T tile[32][33];
   const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
@@ -1746,7 +1756,7 @@ __global__ void transpose_kernel(const T* in, int rows, int cols, T* out, int la
   __syncthreads();
   for (int j = ty; j < 32; j += 8) {
     const int n = bx + j, k = by + tx;  // output row n (input column), column k
-    if (n < cols && k < rows) out[packed_offset(n, k, cols, rows, layout)] = tile[tx][j];
+    if (n < cols && k < rows) out[packed_offset(row0 + n, k, ntot, rows, layout)] = tile[tx][j];
   }
 }
 
@@ -1763,9 +1773,10 @@ __global__ void pack_rows_kernel(const char* in, size_t ld_bytes, int N, int K, 
         *(const u32x4_t*)(src + (size_t)k * esz);
 }
 
-__global__ void pack_vec_kernel(const float* in, int N, float* out, int layout) {
+__global__ void pack_vec_kernel(const float* in, int N, float* out, int layout, int row0,
+                                int ntot) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n < N) out[packed_row(n, N, layout)] = in[n];
+  if (n < N) out[packed_row(row0 + n, ntot, layout)] = in[n];
 }
 
 hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, void* out,
@@ -1777,26 +1788,32 @@ hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, voi
   return hipGetLastError();
 }
 
-hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t s) {
-  hipLaunchKernelGGL(pack_vec_kernel, dim3((N + 255) / 256), dim3(256), 0, s, in, N, out, layout);
+hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t s,
+                               int row0, int ntot) {
+  if (ntot <= 0) ntot = N;
+  if (row0 < 0 || row0 + N > ntot) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_vec_kernel, dim3((N + 255) / 256), dim3(256), 0, s, in, N, out, layout,
+                     row0, ntot);
   return hipGetLastError();
 }
 
 hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
-                            int layout, hipStream_t s) {
+                            int layout, hipStream_t s, int row0, int ntot) {
+  if (ntot <= 0) ntot = cols;
+  if (row0 < 0 || row0 + cols > ntot) return hipErrorInvalidValue;
   dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(256);
   switch (dtype) {
     case F32:
       hipLaunchKernelGGL(transpose_kernel<float>, grid, block, 0, s, (const float*)in, rows, cols,
-                         (float*)out, layout);
+                         (float*)out, layout, row0, ntot);
       break;
     case F16:
       hipLaunchKernelGGL(transpose_kernel<_Float16>, grid, block, 0, s, (const _Float16*)in,
-                         rows, cols, (_Float16*)out, layout);
+                         rows, cols, (_Float16*)out, layout, row0, ntot);
       break;
     case BF16:
       hipLaunchKernelGGL(transpose_kernel<__bf16>, grid, block, 0, s, (const __bf16*)in, rows,
-                         cols, (__bf16*)out, layout);
+                         cols, (__bf16*)out, layout, row0, ntot);
       break;
     default: return hipErrorInvalidValue;
   }

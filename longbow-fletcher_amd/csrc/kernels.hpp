@@ -120,6 +120,13 @@ bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bia
 // for the 4-wave kernels).
 int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias);
 
+// The output width a model uses for a 16-bit projection of N outputs: N, or
+// the next multiple of 256 when the four-wave kernel takes that width and N
+// does not (STORE / GELU / tanh epilogues).  The padding rows of the packed
+// weights and bias are zero, so the extra output columns hold zeros (or the
+// activation of zero) and are never read.
+int gemm_padded_width(int dtype, int N, int K, int epi_kind, int math, bool has_bias);
+
 // C[M, N] = A[M, K] * B[N, K]^T with the epilogue.  MFMA path; requires
 // N % 64 == 0, K % 64 (16-bit) or K % 32 (fp32) == 0 and 16-byte aligned rows,
 // and B packed as epi.layout says.
@@ -135,16 +142,19 @@ hipError_t launch_gemm_generic(int dtype, int trans_a, int trans_b, int M, int N
                                void* C, int ldc, const float* bias, int act, int math,
                                hipStream_t stream);
 
-// Packed (n, k) = in[k, n] (dtype elements, packed_offset): [rows = K,
-// cols = N] to a packed [N, K] weight matrix.
+// Packed (row0 + n, k) = in[k, n] (dtype elements, packed_offset): [rows =
+// K, cols = N] into rows [row0, row0 + N) of a packed [ntot, K] weight matrix
+// (ntot 0: N).
 hipError_t launch_transpose(int dtype, const void* in, int rows, int cols, void* out,
-                            int layout, hipStream_t stream);
+                            int layout, hipStream_t stream, int row0 = 0, int ntot = 0);
 // Packed (n, :) = in[n, :] (packed_offset) for an [N, K] matrix with row
 // stride ld.
 hipError_t launch_pack_rows(int dtype, const void* in, int ld, int N, int K, void* out,
                             int layout, hipStream_t stream);
-// out[packed_row(n)] = in[n] for an fp32 vector of N.
-hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t stream);
+// out[packed_row(row0 + n)] = in[n] for an fp32 vector of N, the packed
+// vector having ntot entries (0: N).
+hipError_t launch_pack_vec_f32(const float* in, int N, float* out, int layout, hipStream_t stream,
+                               int row0 = 0, int ntot = 0);
 
 // ---- attention ------------------------------------------------------------
 // One query block of one (sequence, head).  The sequence's first row and
@@ -180,10 +190,10 @@ hipError_t launch_attention_generic(int dtype, const void* q, const void* k, con
 // ---- normalisation / embedding ---------------------------------------------
 // t = LN(t [+ residual]) row-wise, fp32 statistics; gamma/beta fp32.
 // t_tiled: t is stored tiled (tiled_act_offset; 16-bit, cols % 256 == 0,
-// cols <= 1024), the residual row-major.
+// cols <= 1024), the residual row-major with row stride ld_res (0: cols).
 hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
                             const float* gamma, const float* beta, float eps,
-                            hipStream_t stream, bool t_tiled = false);
+                            hipStream_t stream, bool t_tiled = false, int ld_res = 0);
 // x[t] = LN(word[ids[t]] + pos[pos_ids[t]] (if pos) + type[0]).  Ids outside
 // [0, vocab) read row 0 and set *bad_id (never an out-of-bounds read).
 hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,

@@ -28,15 +28,15 @@
 namespace fl {
 
 struct LayerW {
-  void* wqkv = nullptr;  // [3H, H]
-  float* bqkv = nullptr; // [3H]
-  void* wo = nullptr;    // [H, H]
+  void* wqkv = nullptr;  // [Nqkv, H] (rows past 3H zero)
+  float* bqkv = nullptr; // [Nqkv]
+  void* wo = nullptr;    // [Nh, H]
   float* bo = nullptr;
   float* ln1_g = nullptr;
   float* ln1_b = nullptr;
   void* wi = nullptr;    // [Ni, H] (SwiGLU interleaved)
   float* bi = nullptr;   // [Ni] (same order)
-  void* wd = nullptr;    // [H, I]
+  void* wd = nullptr;    // [Nh, I]
   float* bd = nullptr;
   float* ln2_g = nullptr;
   float* ln2_b = nullptr;
@@ -106,6 +106,10 @@ struct fl_model {
   fl_context* ctx = nullptr;
   fl_model_config cfg{};
   int H = 0, I = 0, Ni = 0, heads = 0, hd = 0, dtype = 0;
+  // Output widths of the QKV projection and of the two H-wide projections
+  // (O, FFN-down): 3H and H, or padded to whole 256-column tiles for the
+  // four-wave GEMM (gemm_padded_width); QKV and TMP have these row strides.
+  int Nqkv = 0, Nh = 0;
   size_t esz = 2;
   bool swiglu = false, rope = false;
   bool mfma_qkv = false, mfma_o = false, mfma_up = false, mfma_down = false;
@@ -279,11 +283,11 @@ int ensure_capacity(fl_model* m, Lane& L, int64_t T, int nseq, size_t nwork, siz
     untrack_free(m, L.pos32);
     // Rows rounded up to whole 256-row tiles (tiled activations, padded GEMM outputs).
     int64_t cap = (std::max<int64_t>(T, 256) + 255) / 256 * 256;
-    const int64_t wide = std::max<int64_t>(3 * m->H, m->Ni);
+    const int64_t wide = std::max<int64_t>(m->Nqkv, m->Ni);
     M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.X));
     M_ST(track_alloc(m, (size_t)cap * wide * m->esz, L.QKV));
     M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.CTX));
-    M_ST(track_alloc(m, (size_t)cap * m->H * m->esz, L.TMP));
+    M_ST(track_alloc(m, (size_t)cap * m->Nh * m->esz, L.TMP));
     if (m->swiglu && !m->mfma_up) M_ST(track_alloc(m, (size_t)cap * m->Ni * m->esz, L.G2));
     M_ST(track_alloc(m, (size_t)cap * 4, L.ids32));
     M_ST(track_alloc(m, (size_t)cap * 4, L.pos32));
@@ -464,9 +468,9 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
         e.rope_cs_q = L.rope_cs_q;
       }
       e.a_tiled = e.c_padded = m->x_tiled;
-      M_ST(gemm(m, L, m->mfma_qkv, L.X, w.wqkv, L.QKV, Ti, 3 * H, H, e));
+      M_ST(gemm(m, L, m->mfma_qkv, L.X, w.wqkv, L.QKV, Ti, m->Nqkv, H, e));
       if (m->rope && !m->rope_fused)
-        M_CHECK(launch_rope(dt, L.QKV, Ti, 2 * m->heads, m->hd, 3 * H, L.pos32, L.rope_cs, s));
+        M_CHECK(launch_rope(dt, L.QKV, Ti, 2 * m->heads, m->hd, m->Nqkv, L.pos32, L.rope_cs, s));
     }
     {
       ProfScope ps(m, L, P_ATTN);
@@ -477,14 +481,14 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
       // XCD groups of two (sequence, head) pairs' query blocks: measured 2%
       // faster than one pair at 512 tokens (the kernel clamps groups at 32).
       if ((m->hd == 64 || m->hd == 32) && dt != FL_F32)
-        M_CHECK(launch_attention_flash(dt, q, k, v, 3 * H, L.CTX, H, L.cu, L.work, L.n_work,
+        M_CHECK(launch_attention_flash(dt, q, k, v, m->Nqkv, L.CTX, H, L.cu, L.work, L.n_work,
                                        m->hd, scale, L.waves, m->q_prescaled, 2 * L.qblocks, s));
       else if (m->hd == 64)
-        M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, 3 * H,
+        M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, m->Nqkv,
                                      (float*)L.CTX, H, L.cu, L.work, L.n_work, scale,
                                      m->cfg.math, s));
       else
-        M_CHECK(launch_attention_generic(dt, q, k, v, 3 * H, L.CTX, H, L.cu, nseq, L.max_len,
+        M_CHECK(launch_attention_generic(dt, q, k, v, m->Nqkv, L.CTX, H, L.cu, nseq, L.max_len,
                                          m->heads, m->hd, scale, m->cfg.math, s));
     }
     {
@@ -492,12 +496,12 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bo : nullptr;
       e.layout = m->lay_o;
-      M_ST(gemm(m, L, m->mfma_o, L.CTX, w.wo, L.TMP, Ti, H, H, e));
+      M_ST(gemm(m, L, m->mfma_o, L.CTX, w.wo, L.TMP, Ti, m->Nh, H, e));
     }
     {
       ProfScope ps(m, L, P_LN);
       M_CHECK(launch_layernorm(dt, L.X, L.TMP, Ti, H, w.ln1_g, w.ln1_b, m->cfg.ln_eps, s,
-                               m->x_tiled));
+                               m->x_tiled, m->Nh));
     }
     {
       ProfScope ps(m, L, P_UP);
@@ -530,12 +534,12 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
       // With X tiled, the SwiGLU output's padding rows come from X's padding
       // rows (no copies of row T-1): FFN-down writes its own padding rows.
       e.c_padded = m->x_tiled;
-      M_ST(gemm(m, L, m->mfma_down, L.QKV, w.wd, L.TMP, Ti, H, m->I, e));
+      M_ST(gemm(m, L, m->mfma_down, L.QKV, w.wd, L.TMP, Ti, m->Nh, m->I, e));
     }
     {
       ProfScope ps(m, L, P_LN);
       M_CHECK(launch_layernorm(dt, L.X, L.TMP, Ti, H, w.ln2_g, w.ln2_b, m->cfg.ln_eps, s,
-                               m->x_tiled));
+                               m->x_tiled, m->Nh));
     }
   }
   {
@@ -605,10 +609,22 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
   m->dtype = c.dtype;
   m->esz = dtype_size(c.dtype);
   m->rope = c.position == FL_POS_ROPE;
-  m->mfma_qkv = mfma_shape_ok(m->dtype, 3 * m->H, m->H);
-  m->mfma_o = mfma_shape_ok(m->dtype, m->H, m->H);
+  {
+    // Widths that are not whole 256-column tiles (MiniLM's 384 and 1152) run
+    // padded: zero weight rows up to the next tile, outputs with that row
+    // stride.  RoPE QKV projections stay unpadded (their epilogue rotates
+    // fixed column ranges).
+    const bool has_bias = c.has_bias != 0;
+    m->Nqkv = m->rope ? 3 * m->H
+                      : gemm_padded_width(m->dtype, 3 * m->H, m->H, EPI_STORE, c.math, has_bias);
+    m->Nh = gemm_padded_width(m->dtype, m->H, m->H, EPI_STORE, c.math, has_bias);
+    if (gemm_padded_width(m->dtype, m->H, m->I, EPI_STORE, c.math, has_bias) != m->Nh)
+      m->Nh = m->H;
+  }
+  m->mfma_qkv = mfma_shape_ok(m->dtype, m->Nqkv, m->H);
+  m->mfma_o = mfma_shape_ok(m->dtype, m->Nh, m->H);
   m->mfma_up = mfma_shape_ok(m->dtype, m->Ni, m->H) && (!m->swiglu || m->I % 16 == 0);
-  m->mfma_down = mfma_shape_ok(m->dtype, m->H, m->I);
+  m->mfma_down = mfma_shape_ok(m->dtype, m->Nh, m->I);
   m->rope_fused = m->mfma_qkv && m->hd == 64;
   {
     const bool has_bias = c.has_bias != 0;
@@ -617,13 +633,13 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
       const int l = gemm_pp_layout(m->dtype, N, K, kind, c.math, has_bias);
       return l >= 0 ? l : fallback;
     };
-    m->lay_qkv = pick(m->mfma_qkv, 3 * m->H, m->H, m->rope && m->rope_fused ? EPI_ROPE : EPI_STORE,
-                      PACK_PLAIN);
-    m->lay_o = pick(m->mfma_o, m->H, m->H, EPI_STORE, PACK_PLAIN);
+    m->lay_qkv = pick(m->mfma_qkv, m->Nqkv, m->H,
+                      m->rope && m->rope_fused ? EPI_ROPE : EPI_STORE, PACK_PLAIN);
+    m->lay_o = pick(m->mfma_o, m->Nh, m->H, EPI_STORE, PACK_PLAIN);
     m->lay_up = m->swiglu ? pick(m->mfma_up, m->Ni, m->H, EPI_SWIGLU, PACK_SWIGLU16)
                           : pick(m->mfma_up, m->Ni, m->H, EPI_GELU, PACK_PLAIN);
     if (m->swiglu && !m->mfma_up) m->lay_up = PACK_PLAIN;
-    m->lay_down = pick(m->mfma_down, m->H, m->I, EPI_STORE, PACK_PLAIN);
+    m->lay_down = pick(m->mfma_down, m->Nh, m->I, EPI_STORE, PACK_PLAIN);
     // The flash kernel takes Q pre-scaled when the QKV projection runs on the
     // ping-pong kernel, whose epilogue applies the scale.
     m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
@@ -635,7 +651,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
                                  true);
     const int qkv_kind = m->rope && m->rope_fused ? EPI_ROPE : EPI_STORE;
     m->x_tiled = m->ffn_tiled && m->lay_qkv >= PACK_LANE16 && m->H % 256 == 0 && m->H <= 1024 &&
-                 gemm_tiled_ok(m->dtype, 3 * m->H, m->H, qkv_kind, c.math, has_bias, false, true,
+                 gemm_tiled_ok(m->dtype, m->Nqkv, m->H, qkv_kind, c.math, has_bias, false, true,
                                true) &&
                  gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, true,
                                false);
@@ -662,11 +678,12 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     if ((st = fill_f32(&m->emb_g, H, 1.f)) || (st = fill_f32(&m->emb_b, H, 0.f))) break;
     m->layers.resize(c.layers);
     for (auto& L : m->layers) {
-      if ((st = zeros(&L.wqkv, 3 * H * H * m->esz)) || (st = fill_f32(&L.bqkv, 3 * H, 0.f)) ||
-          (st = zeros(&L.wo, H * H * m->esz)) || (st = fill_f32(&L.bo, H, 0.f)) ||
+      const size_t Nq = m->Nqkv, Nh = m->Nh;
+      if ((st = zeros(&L.wqkv, Nq * H * m->esz)) || (st = fill_f32(&L.bqkv, Nq, 0.f)) ||
+          (st = zeros(&L.wo, Nh * H * m->esz)) || (st = fill_f32(&L.bo, Nh, 0.f)) ||
           (st = fill_f32(&L.ln1_g, H, 1.f)) || (st = fill_f32(&L.ln1_b, H, 0.f)) ||
           (st = zeros(&L.wi, Ni * H * m->esz)) || (st = fill_f32(&L.bi, Ni, 0.f)) ||
-          (st = zeros(&L.wd, H * I * m->esz)) || (st = fill_f32(&L.bd, H, 0.f)) ||
+          (st = zeros(&L.wd, Nh * I * m->esz)) || (st = fill_f32(&L.bd, Nh, 0.f)) ||
           (st = fill_f32(&L.ln2_g, H, 1.f)) || (st = fill_f32(&L.ln2_b, H, 0.f)))
         break;
     }
@@ -750,15 +767,16 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
     M_CHECK(hipMemcpyAsync(dst, f32, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
     return FL_OK;
   };
-  // [in, out] reference matrix -> [out, in] packed (optionally SwiGLU interleaved)
-  auto pack = [&](void* dst, int rows, int cols, int layout) -> int {
+  // [in, out] reference matrix -> rows [row0, row0 + out) of a packed
+  // [ntot, in] matrix (optionally SwiGLU interleaved).
+  auto pack = [&](void* dst, int rows, int cols, int layout, int row0, int ntot) -> int {
     M_CHECK(launch_cast(f32, FL_F32, cvt, dt, n, 0, s));
-    M_CHECK(launch_transpose(dt, cvt, rows, cols, dst, layout, s));
+    M_CHECK(launch_transpose(dt, cvt, rows, cols, dst, layout, s, row0, ntot));
     return FL_OK;
   };
   // fp32 bias vector in the packed row order of its weights.
-  auto pack_bias = [&](float* dst, int N, int layout) -> int {
-    M_CHECK(launch_pack_vec_f32(f32, N, dst, layout, s));
+  auto pack_bias = [&](float* dst, int N, int layout, int row0, int ntot) -> int {
+    M_CHECK(launch_pack_vec_f32(f32, N, dst, layout, s, row0, ntot));
     return FL_OK;
   };
   if (!per_layer) {
@@ -775,7 +793,6 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
     else return fail(FL_ERR_INVALID, "unknown weight " + nm);
   } else {
     LayerW& L = m->layers[layer];
-    const size_t esz = m->esz;
     // A model created without biases (Nomic) never reads them: a projection
     // bias that is not zero is refused, as the weight-file loaders do.
     const bool proj_bias = field == "q_b" || field == "k_b" || field == "v_b" ||
@@ -787,24 +804,31 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
     if (field == "q_w" || field == "k_w" || field == "v_w") {
       M_ST(expect(H * H));
       const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
-      // The packed orders permute within 64-row blocks, so each part packs alone.
-      M_ST(pack((char*)L.wqkv + (size_t)part * H * H * esz, (int)H, (int)H, m->lay_qkv));
+      // Rows [part * H, part * H + H) of the packed [Nqkv, H] matrix.
+      M_ST(pack(L.wqkv, (int)H, (int)H, m->lay_qkv, part * (int)H, m->Nqkv));
     } else if (field == "q_b" || field == "k_b" || field == "v_b") {
       M_ST(expect(H));
       const int part = field[0] == 'q' ? 0 : (field[0] == 'k' ? 1 : 2);
-      M_ST(pack_bias(L.bqkv + part * H, (int)H, m->lay_qkv));
-    } else if (field == "o_w") { M_ST(expect(H * H)); M_ST(pack(L.wo, (int)H, (int)H, m->lay_o)); }
-    else if (field == "o_b") { M_ST(expect(H)); M_ST(pack_bias(L.bo, (int)H, m->lay_o)); }
+      M_ST(pack_bias(L.bqkv, (int)H, m->lay_qkv, part * (int)H, m->Nqkv));
+    } else if (field == "o_w") {
+      M_ST(expect(H * H));
+      M_ST(pack(L.wo, (int)H, (int)H, m->lay_o, 0, m->Nh));
+    } else if (field == "o_b") { M_ST(expect(H)); M_ST(pack_bias(L.bo, (int)H, m->lay_o, 0, m->Nh)); }
     else if (field == "attn_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_g)); }
     else if (field == "attn_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln1_b)); }
     else if (field == "inter_w") {
       M_ST(expect(H * Ni));
-      M_ST(pack(L.wi, (int)H, (int)Ni, m->lay_up));
+      M_ST(pack(L.wi, (int)H, (int)Ni, m->lay_up, 0, (int)Ni));
     } else if (field == "inter_b") {
       M_ST(expect(Ni));
-      M_ST(pack_bias(L.bi, (int)Ni, m->lay_up));
-    } else if (field == "out_w") { M_ST(expect(I * H)); M_ST(pack(L.wd, (int)I, (int)H, m->lay_down)); }
-    else if (field == "out_b") { M_ST(expect(H)); M_ST(pack_bias(L.bd, (int)H, m->lay_down)); }
+      M_ST(pack_bias(L.bi, (int)Ni, m->lay_up, 0, (int)Ni));
+    } else if (field == "out_w") {
+      M_ST(expect(I * H));
+      M_ST(pack(L.wd, (int)I, (int)H, m->lay_down, 0, m->Nh));
+    } else if (field == "out_b") {
+      M_ST(expect(H));
+      M_ST(pack_bias(L.bd, (int)H, m->lay_down, 0, m->Nh));
+    }
     else if (field == "out_ln_g") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_g)); }
     else if (field == "out_ln_b") { M_ST(expect(H)); M_ST(copy_f32(L.ln2_b)); }
     else return fail(FL_ERR_INVALID, "unknown weight " + nm);

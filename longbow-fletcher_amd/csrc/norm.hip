@@ -102,13 +102,13 @@ __device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], i
 
 template <typename T, int NCH, int VEC>
 __global__ void __launch_bounds__(256)
-layernorm_kernel(T* t, const T* residual, int rows, int cols, const float* gamma,
+layernorm_kernel(T* t, const T* residual, int ldr, int rows, int cols, const float* gamma,
                  const float* beta, float eps) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   T* tr = t + (size_t)row * cols;
-  const T* rr = residual ? residual + (size_t)row * cols : nullptr;
+  const T* rr = residual ? residual + (size_t)row * ldr : nullptr;
   float x[NCH][VEC];
   bool valid[NCH];
   int col0[NCH];
@@ -140,13 +140,13 @@ layernorm_kernel(T* t, const T* residual, int rows, int cols, const float* gamma
 // wave covers whole 128-byte lines of the tiled blocks.
 template <typename T, int LPR, int NCH, int VEC, bool TT>
 __global__ void __launch_bounds__(256)
-layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* gamma,
+layernorm_rows_kernel(T* t, const T* residual, int ldr, int rows, int cols, const float* gamma,
                       const float* beta, float eps) {
   constexpr int RPW = 64 / LPR;
   const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + ((threadIdx.x & 63) / LPR);
   const int lane = threadIdx.x % LPR;
   if (row >= rows) return;
-  const T* rr = residual ? residual + (size_t)row * cols : nullptr;
+  const T* rr = residual ? residual + (size_t)row * ldr : nullptr;
   float x[NCH][VEC];
   bool valid[NCH];
   int col0[NCH];
@@ -176,67 +176,79 @@ layernorm_rows_kernel(T* t, const T* residual, int rows, int cols, const float* 
 }
 
 template <typename T, int LPR, int NCH, int VEC>
-static hipError_t ln_rows_launch(void* t, const void* res, int rows, int cols, const float* g,
-                                 const float* b, float eps, hipStream_t s, bool tiled) {
+static hipError_t ln_rows_launch(void* t, const void* res, int ldr, int rows, int cols,
+                                 const float* g, const float* b, float eps, hipStream_t s,
+                                 bool tiled) {
   constexpr int rows_per_block = 4 * (64 / LPR);
   const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
   if (tiled)
     hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, true>), grid, dim3(256), 0, s,
-                       (T*)t, (const T*)res, rows, cols, g, b, eps);
+                       (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
   else
     hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, false>), grid, dim3(256), 0, s,
-                       (T*)t, (const T*)res, rows, cols, g, b, eps);
+                       (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
   return hipGetLastError();
 }
 
 template <typename T, int NCH, int VEC>
-static hipError_t ln_launch(void* t, const void* res, int rows, int cols, const float* g,
+static hipError_t ln_launch(void* t, const void* res, int ldr, int rows, int cols, const float* g,
                             const float* b, float eps, hipStream_t s) {
   hipLaunchKernelGGL((layernorm_kernel<T, NCH, VEC>), dim3((rows + 3) / 4), dim3(256), 0, s,
-                     (T*)t, (const T*)res, rows, cols, g, b, eps);
+                     (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
   return hipGetLastError();
 }
 
+// ldr: row stride of the residual (elements).
 template <typename T>
-static hipError_t ln_typed(void* t, const void* res, int rows, int cols, const float* g,
-                           const float* b, float eps, hipStream_t s, bool tiled) {
+static hipError_t ln_typed(void* t, const void* res, int ldr, int rows, int cols,
+                           const float* g, const float* b, float eps, hipStream_t s, bool tiled) {
   constexpr int V16 = 16 / sizeof(T);  // elements per 16-byte vector
-  if (cols % (32 * V16) == 0 && cols <= 4 * 32 * V16 &&
-      (((uintptr_t)t | (uintptr_t)res) % 16) == 0) {
+  const bool a16 = (((uintptr_t)t | (uintptr_t)res | ((size_t)ldr * sizeof(T))) % 16) == 0;
+  if (cols % (32 * V16) == 0 && cols <= 4 * 32 * V16 && a16) {
     switch (cols / (32 * V16)) {
-      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, rows, cols, g, b, eps, s, tiled);
-      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, rows, cols, g, b, eps, s, tiled);
-      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, rows, cols, g, b, eps, s, tiled);
-      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, rows, cols, g, b, eps, s, tiled);
+      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
+      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
+      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
+      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
     }
   }
+  // Widths of 3 x 16 vectors (384 in 16 bits: MiniLM): 16 lanes per row.
+  if (sizeof(T) == 2 && !tiled && cols == 3 * 16 * V16 && a16)
+    return ln_rows_launch<T, 16, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, false);
   if (tiled) return hipErrorInvalidValue;
-  if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res) % (4 * sizeof(T)) == 0)) {
+  if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res | ((size_t)ldr * sizeof(T))) %
+                        (4 * sizeof(T))) == 0) {
     const int nch = (cols / 4 + 63) / 64;
-    if (nch <= 1) return ln_launch<T, 1, 4>(t, res, rows, cols, g, b, eps, s);
-    if (nch <= 2) return ln_launch<T, 2, 4>(t, res, rows, cols, g, b, eps, s);
-    if (nch <= 3) return ln_launch<T, 3, 4>(t, res, rows, cols, g, b, eps, s);
-    if (nch <= 4) return ln_launch<T, 4, 4>(t, res, rows, cols, g, b, eps, s);
-    if (nch <= 8) return ln_launch<T, 8, 4>(t, res, rows, cols, g, b, eps, s);
-    if (nch <= 16) return ln_launch<T, 16, 4>(t, res, rows, cols, g, b, eps, s);
+    if (nch <= 1) return ln_launch<T, 1, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 2) return ln_launch<T, 2, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 3) return ln_launch<T, 3, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 4) return ln_launch<T, 4, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 8) return ln_launch<T, 8, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 16) return ln_launch<T, 16, 4>(t, res, ldr, rows, cols, g, b, eps, s);
     return hipErrorInvalidValue;
   }
   const int nch = (cols + 63) / 64;
-  if (nch <= 2) return ln_launch<T, 2, 1>(t, res, rows, cols, g, b, eps, s);
-  if (nch <= 8) return ln_launch<T, 8, 1>(t, res, rows, cols, g, b, eps, s);
-  if (nch <= 32) return ln_launch<T, 32, 1>(t, res, rows, cols, g, b, eps, s);
+  if (nch <= 2) return ln_launch<T, 2, 1>(t, res, ldr, rows, cols, g, b, eps, s);
+  if (nch <= 8) return ln_launch<T, 8, 1>(t, res, ldr, rows, cols, g, b, eps, s);
+  if (nch <= 32) return ln_launch<T, 32, 1>(t, res, ldr, rows, cols, g, b, eps, s);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
                             const float* gamma, const float* beta, float eps,
-                            hipStream_t stream, bool t_tiled) {
+                            hipStream_t stream, bool t_tiled, int ld_res) {
   if (rows <= 0) return hipSuccess;
   if (t_tiled && (dtype == F32 || cols % 256)) return hipErrorInvalidValue;
+  if (ld_res <= 0) ld_res = cols;
+  if (ld_res < cols) return hipErrorInvalidValue;
   switch (dtype) {
-    case F32: return ln_typed<float>(t, residual, rows, cols, gamma, beta, eps, stream, false);
-    case F16: return ln_typed<_Float16>(t, residual, rows, cols, gamma, beta, eps, stream, t_tiled);
-    case BF16: return ln_typed<__bf16>(t, residual, rows, cols, gamma, beta, eps, stream, t_tiled);
+    case F32:
+      return ln_typed<float>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream, false);
+    case F16:
+      return ln_typed<_Float16>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream,
+                                t_tiled);
+    case BF16:
+      return ln_typed<__bf16>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream, t_tiled);
   }
   return hipErrorInvalidValue;
 }
