@@ -457,8 +457,8 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
   note_write(ctx, c);
   GemmEpilogue epi;
   if (!trans_a && alpha == 1.0f) {
-    // The ping-pong kernel takes B packed [n x k] in its own row order.
-    const int lay = gemm_pp_layout(dtype, n, k, EPI_STORE, FL_MATH_EXACT, false);
+    // The four-wave kernel takes B packed [n x k] in its own row order.
+    const int lay = gemm_w4_layout(dtype, n, k, EPI_STORE, FL_MATH_EXACT, false);
     const size_t esz = dtype_size(dtype);
     const bool rows_ok = trans_b && !(((uintptr_t)b | ((size_t)ldb * esz)) & 15);
     if (lay >= 0 && ((!trans_b && ldb == n) || rows_ok)) {
@@ -521,13 +521,13 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   // Scratch layout: [fp32 bias][packed W][unfused product]
   const size_t bias_bytes = bias ? ((size_t)out_cols * 4 + 255) / 256 * 256 : 0;
   const size_t w_bytes = ((size_t)out_cols * in_cols * esz + 255) / 256 * 256;
-  // SwiGLU runs in the ping-pong kernel's epilogue when that kernel takes the
+  // SwiGLU runs in the four-wave kernel's epilogue when that kernel takes the
   // shape (16-bit, exact math); otherwise the full product is written first.
   const bool w_rows_ok =
       w_layout == FL_W_IN_OUT || !(((uintptr_t)w | ((size_t)in_cols * esz)) & 15);
   const bool fused_swiglu =
       act == FL_ACT_SWIGLU && w_rows_ok && !(((uintptr_t)x | (uintptr_t)out) & 15) &&
-      gemm_pp_layout(dtype, out_cols, in_cols, EPI_SWIGLU, math, bias != nullptr) >= 0;
+      gemm_w4_layout(dtype, out_cols, in_cols, EPI_SWIGLU, math, bias != nullptr) >= 0;
   const bool unfused = (act == FL_ACT_SWIGLU && !fused_swiglu) || act == FL_ACT_SOFTMAX;
   const size_t y_bytes = unfused ? (size_t)rows * out_cols * esz : 0;
   int st;
@@ -542,8 +542,8 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
                           : (epi_act == FL_ACT_GELU ? EPI_GELU
                                                     : (epi_act == FL_ACT_TANH ? EPI_TANH : EPI_STORE));
   epi.math = math;
-  // The ping-pong kernel takes W and the bias in its own row order.
-  const int lay = gemm_pp_layout(dtype, out_cols, in_cols, epi.kind, math, bias != nullptr);
+  // The four-wave kernel takes W and the bias in its own row order.
+  const int lay = gemm_w4_layout(dtype, out_cols, in_cols, epi.kind, math, bias != nullptr);
   epi.layout = lay >= 0 && w_rows_ok ? lay : PACK_PLAIN;
   const int ldy = fused_swiglu ? out_cols / 2 : out_cols;
   const void* wnk = w;

@@ -20,10 +20,6 @@
 namespace fl {
 
 // Tuning constants, chosen by measurement on MI355X.
-// Ping-pong kernel (16-bit, N % 256 == 0, the layouts the four-wave kernel
-// does not take): K step, LDS stages, and the SwiGLU output staging (KB per
-// wave) that sets how many row blocks are stored per compute tick.
-constexpr int kPpBK = 32, kPpNS = 4, kPpSpread = 8;
 // Row blocks per group of the persistent tile order (an XCD's workgroups
 // share a group's activation rows in L2).
 constexpr int kGroupM = 8;
@@ -502,9 +498,10 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_lds_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Ping-pong epilogue.  B (and the bias) are packed so that the 16 values a
-// lane holds for one row block are adjacent outputs (PackLayout), so each
-// lane stores 16 bytes at a time.  The bias is read in packed order.
+// Four-wave kernel epilogue math.  B (and the bias) are packed so that the 16
+// values a lane holds for one row block are adjacent outputs (PackLayout), so
+// each lane produces 16 contiguous bytes at a time.  The bias is read in
+// packed order.
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ inline u32x4_t pack8(float4_t a, float4_t b) {
@@ -534,7 +531,7 @@ __device__ inline void store8(T* dst, float4_t a, float4_t b) {
 // (a group wholly past rope_cols; rope_at is not called).
 template <typename T, int EPI, int MATH, bool BIAS, bool ROT = true, typename BiasAt,
           typename RopeAt, typename Put>
-__device__ __attribute__((always_inline)) inline void pp_epilogue_block(
+__device__ __attribute__((always_inline)) inline void w4_epilogue_block(
     const GemmParams& p, float4_t (&v)[4], int nbase, int lane, BiasAt&& bias_at,
     RopeAt&& rope_at, Put&& put) {
   const int g = lane >> 4;
@@ -589,428 +586,21 @@ __device__ __attribute__((always_inline)) inline void pp_epilogue_block(
   }
 }
 
-template <typename T, int EPI, int MATH, bool BIAS>
-__device__ __attribute__((always_inline)) inline void pp_epilogue(const GemmParams& p,
-                                                                  const float4_t (&acc)[4][8],
-                                                                  int m0, int nbase, int wm_off,
-                                                                  int lane) {
-  constexpr int TM = 8;
-  // Opaque copy of the lane id: stops lane-dependent epilogue addresses from
-  // being hoisted out of the tile loop into registers.
-  asm volatile("" : "+v"(lane));
-#pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    float4_t v[4] = {acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
-    // Rows past M are computed on row M-1's inputs and not stored.
-    const int m = m0 + wm_off + t * 16 + (lane & 15);
-    const int mc = m < p.M ? m : p.M - 1;
-    T* crow = (T*)p.C + (size_t)m * p.ldc;
-    const int g = lane >> 4;
-    auto bias_at = [&](int f) { return *(const float4_t*)(p.epi.bias + nbase + f * 16 + g * 4); };
-    auto rope_at = [&](int k) {
-      const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
-      return ((const float4_t*)(table + (size_t)p.epi.pos[mc] * 32 + g * 8))[k];
-    };
-    auto put = [&](int col, float4_t a, float4_t b) {
-      if (m < p.M) store8<T>(crow + col, a, b);
-    };
-    if (BIAS && p.epi.bias)
-      pp_epilogue_block<T, EPI, MATH, BIAS>(p, v, nbase, lane, bias_at, rope_at, put);
-    else
-      pp_epilogue_block<T, EPI, MATH, false>(p, v, nbase, lane, bias_at, rope_at, put);
-    // One row block at a time: hoisting every block's table loads would
-    // need more registers than the accumulators leave.
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// SwiGLU epilogue: row blocks t < 8 - NSTG are stored at once; the packed
-// outputs of the last NSTG row blocks go to out + (t - 8 + NSTG)*1024 +
-// lane*16 in LDS, and the kernel stores them to C one row block per compute
-// tick, so a finished tile's stores do not reach the memory pipeline in one
-// burst ahead of the DMA of the next steps.
-template <typename T, int MATH, int NSTG>
-__device__ __attribute__((always_inline)) inline void pp_swiglu_stage(const GemmParams& p,
-                                                                     const float4_t (&acc)[4][8],
-                                                                     int m0, int nbase, int lane,
-                                                                     char* out) {
-  asm volatile("" : "+v"(lane));
-  const int g = lane >> 4;
-  const float* bias = p.epi.bias;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    float4_t o[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      // PACK_SWIGLU_LANE: tiles 2h / 2h+1 are gate / up of outputs 8g+4h+i.
-      float4_t gt = acc[2 * h][t], up = acc[2 * h + 1][t];
-      if (bias) {
-        gt += *(const float4_t*)(bias + nbase + (2 * h) * 16 + g * 4);
-        up += *(const float4_t*)(bias + nbase + (2 * h + 1) * 16 + g * 4);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[h][i] = silu_m<MATH>(gt[i]) * up[i];
-    }
-    u32x4_t v;
-    if constexpr (Elem<T>::dtype == F16) {
-      const half8_t hh = {(_Float16)o[0][0], (_Float16)o[0][1], (_Float16)o[0][2],
-                          (_Float16)o[0][3], (_Float16)o[1][0], (_Float16)o[1][1],
-                          (_Float16)o[1][2], (_Float16)o[1][3]};
-      v = __builtin_bit_cast(u32x4_t, hh);
-    } else {
-      const bf16x8_t hh = {(__bf16)o[0][0], (__bf16)o[0][1], (__bf16)o[0][2], (__bf16)o[0][3],
-                           (__bf16)o[1][0], (__bf16)o[1][1], (__bf16)o[1][2], (__bf16)o[1][3]};
-      v = __builtin_bit_cast(u32x4_t, hh);
-    }
-    if (t >= 8 - NSTG) {
-      *(u32x4_t*)(out + (t - (8 - NSTG)) * 1024 + lane * 16) = v;
-    } else {
-      const int m = m0 + t * 16 + (lane & 15);
-      if (m < p.M) *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + nbase / 2 + g * 8) = v;
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Ping-pong 16-bit GEMM: 256x256 tiles, 8 waves in two groups of four (one
-// wave of each group per SIMD), NS LDS stages of BK-deep K slices, one
-// workgroup per CU walking its tiles as one continuous stream of K steps.
-//
-// Each K step takes two barrier-separated ticks per group: a memory tick
-// (run a pending epilogue, read this step's fragments from LDS into
-// registers, issue the DMA of step s+NS-1) and a compute tick (MFMAs on
-// registers only).  Group 1 runs one tick behind group 0, so on every SIMD
-// one wave issues MFMAs while the other does its memory work.
-//
-// Tick 2s: group 0 reads stage s%NS and issues its half of step s+NS-1 into
-// stage (s-1)%NS; group 1 computes step s-1.  Tick 2s+1: group 0 computes
-// step s; group 1 reads stage s%NS and issues its half of step s+NS-1.
-// Stage (s-1)%NS was last read in tick 2s-1.  At the end of tick 2s+1 each
-// wave waits until its own DMA of step s+1 has landed, so step s+1 is
-// complete in LDS when tick 2s+2 starts.
-//
-// Wave (g, w) owns output rows [128g, 128g+128) x features [64w, 64w+64):
-// the same 128x64 wave tile and epilogue as the 4-wave kernels.  Group 0
-// loads the activation rows, group 1 the weight rows.
-// ---------------------------------------------------------------------------
-__device__ inline void pp_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
 // 16-byte chunk swizzle of an LDS row: the 16 rows of one fragment read
 // land on distinct banks (64-byte rows: pairs of rows share a 128-byte bank
 // line; 128-byte rows: one row per bank line).
 template <int CPR>
-__device__ inline int pp_swz(int row) {
+__device__ inline int w4_swz(int row) {
   if constexpr (CPR == 4) return (row >> 1) & 3;
   else return (row & 7) ^ ((row >> 3) & 1);
-}
-
-template <typename T, int EPI, int MATH, int BK, int NS>
-__global__ void __launch_bounds__(512) gemm_pp_kernel(GemmParams p, int ntiles) {
-  constexpr int BM = 256, BN = 256;
-  constexpr int ROWB = BK * 2;                 // bytes per LDS row
-  constexpr int CPR = BK / 8;                  // 16-byte chunks per row
-  constexpr int RPL = 64 / CPR;                // rows per 1 KB DMA load
-  constexpr int STAGE = (BM + BN) * ROWB;
-  constexpr int KS = BK / 32;                  // MFMA k steps per K step
-  constexpr int TM = 8, FN = 4, WTM = 128, WTN = 64;
-  constexpr int NLD = STAGE / 1024 / 8;        // 1 KB DMA loads per wave per step
-  constexpr int GROUP_M = kGroupM;
-  static_assert(BK == 32 || BK == 64, "BK 32 or 64");
-  // SwiGLU stages NSTG of each wave's 8 finished row blocks in LDS (1 KB
-  // each) and stores them over the following compute ticks.  (Staging half
-  // of the plain STORE epilogue's rows, at the cost of a stage, was slower.)
-  constexpr bool STAGE_OUT = EPI == EPI_SWIGLU;
-  constexpr int NSTG = kPpSpread;
-  constexpr int OUTW = STAGE_OUT ? NSTG * 1024 : 0;
-  static_assert(NS >= 2 && NS * STAGE + 8 * OUTW <= 160 * 1024, "LDS stages");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 8 * OUTW];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2, wn = wave & 3;
-
-  // Persistent tile order: when the tiles split evenly, the workgroups of one
-  // XCD take consecutive runs of the grouped order, so the tiles an XCD has
-  // in flight share activation row-blocks and weight column-blocks in L2.
-  const int G = (int)gridDim.x;
-  const int me = xcd_remap((int)blockIdx.x, G);
-  const int my_tiles = me < ntiles ? (ntiles - 1 - me) / G + 1 : 0;
-  if (my_tiles == 0) return;
-  const bool chunked = (ntiles % G == 0) && (G % 8 == 0);
-  const int per = G / 8;
-  const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
-  const int per_group = GROUP_M * num_n;
-  auto coords = [&](int i, int& m0, int& n0) __attribute__((always_inline)) {
-    const int L = chunked ? (me / per) * (my_tiles * per) + i * per + (me % per) : i * G + me;
-    const int g = L / per_group;
-    const int first_m = g * GROUP_M;
-    const int gsize = min(num_m - first_m, GROUP_M);
-    const int r = L - g * per_group;
-    m0 = (first_m + r % gsize) * BM;
-    n0 = (r / gsize) * BN;
-  };
-  const int nk = p.K / BK;
-  const int total = my_tiles * nk;
-
-  // DMA geometry: wave (g, w) fills rows [RPL*NLD*w, RPL*NLD*(w+1)) of the
-  // activation (g = 0) or weight (g = 1) half of a stage; lane l writes
-  // 16-byte chunk l%CPR of row l/CPR of each 1 KB load, holding global chunk
-  // (l%CPR) ^ swz(row).  Activation rows past M re-read row M-1 (never
-  // stored).
-  // The weights are stored tiled (tiled_offset): a stage's weight half is
-  // one contiguous 16 KB block, already in LDS order.
-  static_assert(BK == 32, "tiled weights hold 32-deep K slices");
-  const int lrow = lane / CPR, lcol = lane % CPR;
-  const size_t kstride = grp == 0 ? BK * sizeof(T) : (size_t)BN * BK * sizeof(T);
-  uint32_t off[NLD];
-  const char* gbase = nullptr;
-  auto load_tile = [&](int ti) __attribute__((always_inline)) {
-    int m0, n0;
-    coords(ti, m0, n0);
-    if (grp == 0) {
-      const int lim = p.M - 1 - m0;
-      gbase = (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) {
-        const int row = (wn * NLD + j) * RPL + lrow;
-        const int c = lcol ^ pp_swz<CPR>(row);
-        off[j] = (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
-      }
-    } else {
-      gbase = (const char*)p.B + (size_t)(n0 / BN) * nk * kstride;
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) off[j] = (uint32_t)((wn * NLD + j) * 1024 + lane * 16);
-    }
-  };
-  // DMA cursor: the step that the next issue loads.  Past the last step it
-  // keeps re-loading slice 0 of the last tile (in bounds, into a stage that
-  // is never read again), so every tick issues the same number of loads and
-  // the wait counts stay uniform.
-  int ld_tile = 0, ld_k = 0;
-  auto issue_one = [&](char* stage, int j) __attribute__((always_inline)) {
-    const char* src = gbase + (size_t)ld_k * kstride;
-    char* dst = stage + grp * (BM * ROWB) + wn * NLD * 1024;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + off[j]),
-                                     (__attribute__((address_space(3))) void*)(dst + j * 1024), 16,
-                                     0, 0);
-  };
-  auto advance = [&]() __attribute__((always_inline)) {
-    if (++ld_k == nk) {
-      ld_k = 0;
-      if (ld_tile + 1 < my_tiles) load_tile(++ld_tile);
-    }
-  };
-  auto issue = [&](char* stage) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) issue_one(stage, j);
-    advance();
-  };
-
-  // Fragment reads: row base + (lane & 15), k chunk 4*ks + (lane >> 4).
-  const int fr = lane & 15, fg = lane >> 4;
-  const int swz = pp_swz<CPR>(fr);
-  const int a_row0 = (grp * WTM + fr) * ROWB;
-  const int b_row0 = BM * ROWB + (wn * WTN + fr) * ROWB;
-  u32x4_t fa[KS][TM], fb[KS][FN];
-  auto read_frags = [&](const char* st) __attribute__((always_inline)) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int co = ((ks * 4 + fg) ^ swz) << 4;
-#pragma unroll
-      for (int t = 0; t < TM; ++t) fa[ks][t] = *(const u32x4_t*)(st + a_row0 + t * 16 * ROWB + co);
-#pragma unroll
-      for (int f = 0; f < FN; ++f) fb[ks][f] = *(const u32x4_t*)(st + b_row0 + f * 16 * ROWB + co);
-    }
-  };
-
-  float4_t acc[FN][TM];
-  // The first K step of a tile multiplies into zero instead of clearing the
-  // accumulators after each epilogue.
-  // Compute tick: the step's MFMAs, with this wave's DMA of step s+NS-1
-  // (into `stage`) issued one load per MFMA group, so the DMA queue fills
-  // gradually instead of in one burst.
-  constexpr int NMF = KS * FN * TM;
-  constexpr int PER = NMF / NLD;
-  static_assert(NMF % NLD == 0, "loads spread evenly over the MFMAs");
-  // Staged outputs not yet stored: staged block NSTG - pst_left is next; its
-  // 16 bytes per lane are read from LDS in the memory tick (pv) and stored
-  // first thing in the following compute tick, ahead of that tick's DMA.
-  char* outw = lds + NS * STAGE + wave * OUTW;
-  int pst_left = 0, pst_row0 = 0, pst_col = 0, stored = 0;
-  u32x4_t pv = {0, 0, 0, 0};
-  auto fetch_pending = [&]() __attribute__((always_inline)) {
-    if constexpr (STAGE_OUT) {
-      if (pst_left > 0) pv = *(const u32x4_t*)(outw + (NSTG - pst_left) * 1024 + lane * 16);
-    }
-  };
-  auto store_pending = [&]() __attribute__((always_inline)) {
-    stored = 0;
-    if constexpr (STAGE_OUT) {
-      if (pst_left > 0) {
-        // staged block NSTG - pst_left is row block TM - pst_left
-        const int m = pst_row0 + (TM - pst_left) * 16 + (lane & 15);
-        if (m < p.M) *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + pst_col) = pv;
-        --pst_left;
-        stored = 1;
-      }
-    }
-  };
-  auto compute = [&](char* stage) __attribute__((always_inline)) {
-    store_pending();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int f = 0; f < FN; ++f)
-#pragma unroll
-        for (int t = 0; t < TM; ++t) {
-          Mfma<T>::mma(acc[f][t], fb[ks][f], fa[ks][t]);
-          const int i = (ks * FN + f) * TM + t;
-          if (i % PER == PER - 1) issue_one(stage, i / PER);
-        }
-    // Interleave PER MFMAs and one DMA load (the RoPE variant leaves the
-    // order to the scheduler: pinning it there costs registers it lacks).
-    if constexpr (EPI != EPI_ROPE) {
-#pragma unroll
-      for (int g = 0; g < NLD; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      }
-    }
-    advance();
-  };
-  auto zero_acc = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int f = 0; f < FN; ++f)
-#pragma unroll
-      for (int t = 0; t < TM; ++t) acc[f][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  };
-  auto epilogue = [&](int ti) __attribute__((always_inline)) {
-    int m0, n0;
-    coords(ti, m0, n0);
-    // The previous tile's NSTG staged row blocks went out in the compute ticks
-    // since its epilogue (gemm_pp_layout requires K / BK >= 8).
-    if constexpr (EPI == EPI_SWIGLU) {
-      pp_swiglu_stage<T, MATH, NSTG>(p, acc, m0 + grp * WTM, n0 + wn * WTN, lane, outw);
-      pst_left = NSTG;
-      pst_row0 = m0 + grp * WTM;
-      pst_col = (n0 + wn * WTN) / 2 + (lane >> 4) * 8;
-    } else {
-      pp_epilogue<T, EPI, MATH, EPI != EPI_ROPE>(p, acc, m0, n0 + wn * WTN, grp * WTM, lane);
-    }
-    zero_acc();
-    // Keep the next fragment reads (and their registers) after the epilogue.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Prologue: steps 0 .. NS-2 into stages 0 .. NS-2.
-  zero_acc();
-  load_tile(0);
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(lds + s * STAGE);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  pp_barrier();
-
-  // DMA wait for step s+1: the loads of one wave complete in issue order and
-  // every tick issues NLD of them, so "step s+1 landed" is "at most the
-  // loads of the NS-2 later steps outstanding".  Epilogue stores also count
-  // in vmcnt; they can only make the wait longer, never shorter.
-  // A compute tick that stored a staged row block issued that store before
-  // its DMA loads, so it too may stay outstanding.
-  auto wait_next = [&]() __attribute__((always_inline)) {
-    if constexpr (STAGE_OUT) {
-      asm volatile(
-          "s_cmp_eq_u32 %0, 0\n"
-          "s_cbranch_scc1 1f\n"
-          "s_waitcnt vmcnt(%1)\n"
-          "s_branch 2f\n"
-          "1:\n"
-          "s_waitcnt vmcnt(%2)\n"
-          "2:" ::"s"(stored),
-          "n"(NLD * (NS - 2) + 1), "n"(NLD * (NS - 2))
-          : "memory", "scc");
-    } else {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD * (NS - 2)) : "memory");
-    }
-  };
-
-  int ck = 0, ctile = 0;       // K step / tile of the next compute
-  bool pending = false;        // accumulators hold a finished tile
-  int ptile = 0;
-  if (grp == 0) {
-    for (int s = 0; s < total; ++s) {
-      // tick 2s: memory tick of step s
-      if (pending) {
-        epilogue(ptile);
-        pending = false;
-      }
-      read_frags(lds + (s % NS) * STAGE);
-      fetch_pending();
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      pp_barrier();
-      // tick 2s+1: compute step s, DMA of step s+NS-1
-      compute(lds + ((s + NS - 1) % NS) * STAGE);
-      if (++ck == nk) {
-        ck = 0;
-        pending = true;
-        ptile = ctile++;
-      }
-      wait_next();
-      pp_barrier();
-    }
-  } else {
-    for (int s = 0; s < total; ++s) {
-      // tick 2s: compute step s-1, DMA of step s+NS-1
-      char* nxt = lds + ((s + NS - 1) % NS) * STAGE;
-      if (s > 0) {
-        compute(nxt);
-        if (++ck == nk) {
-          ck = 0;
-          pending = true;
-          ptile = ctile++;
-        }
-      } else {
-        issue(nxt);
-      }
-      pp_barrier();
-      // tick 2s+1: memory tick of step s.  With an epilogue, wait for the
-      // DMA first so the wait does not include the new stores.
-      if (pending) {
-        wait_next();
-        epilogue(ptile);
-        pending = false;
-        read_frags(lds + (s % NS) * STAGE);
-        fetch_pending();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      } else {
-        read_frags(lds + (s % NS) * STAGE);
-        fetch_pending();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        wait_next();
-      }
-      pp_barrier();
-    }
-    compute(lds + ((total + NS - 1) % NS) * STAGE);  // its DMA is a dummy reload
-    pending = true;
-    ptile = ctile;
-  }
-  if (pending) epilogue(ptile);
-#pragma unroll
-  for (int t = 0; t < NSTG; ++t) {
-    fetch_pending();
-    store_pending();
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
 // Four-wave 16-bit GEMM: 256x256 tiles, one wave per SIMD, each wave owning a
 // 128x128 output block (64 accumulator tiles in AGPRs), NS LDS stages of
-// 32-deep K slices in the ping-pong kernel's layout (same packed weights,
-// same epilogues).  Against the ping-pong kernel's 128x64 wave tiles this
-// reads a third fewer bytes from LDS per MFMA and needs one barrier per K
-// step instead of two; the price is that nothing hides the epilogue.
+// 32-deep K slices of weights packed tiled (packed_offset).  Against 128x64
+// wave tiles (eight waves, two per SIMD) this reads a third fewer bytes from
+// LDS per MFMA; the price is that nothing hides the epilogue.
 //
 // A K step is written out as volatile asm: 64 MFMAs, interleaved with the 16
 // LDS fragment reads of the next step (into the other register set) and the
@@ -1105,7 +695,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = wave * 64 + j * 16 + lrow;
-      const int c = lcol ^ pp_swz<4>(row);
+      const int c = lcol ^ w4_swz<4>(row);
       off[j] = a_tiled ? (uint32_t)((wave * 4 + j) * 1024 + lane * 16)
                        : (uint32_t)(min(row, lim) * p.lda + c * 8) * (uint32_t)sizeof(T);
       off[4 + j] = (uint32_t)((wave * 4 + j) * 1024 + lane * 16);
@@ -1115,7 +705,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // Fragment reads: A block t is rows 128*wm + 16t + (lane & 15), B block f
   // rows 128*wn + 16f + (lane & 15), 16-byte k chunk lane >> 4 (swizzled).
   const int fr = lane & 15, fg = lane >> 4;
-  const uint32_t co = (uint32_t)((fg ^ pp_swz<4>(fr)) << 4);
+  const uint32_t co = (uint32_t)((fg ^ w4_swz<4>(fr)) << 4);
   const uint32_t rdA = lds0 + (uint32_t)((wm * 128 + fr) * ROWB) + co;
   const uint32_t rdB = lds0 + (uint32_t)(BM * ROWB + (wn * 128 + fr) * ROWB) + co;
   const uint32_t dma0 = lds0 + (uint32_t)wave * 4096;
@@ -1311,7 +901,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
           v[2] = W4Acc<(4 * h + 2) * 8 + t>::read();
           v[3] = W4Acc<(4 * h + 3) * 8 + t>::read();
         }
-        pp_epilogue_block<T, EPI, MATH, HB, ROT>(
+        w4_epilogue_block<T, EPI, MATH, HB, ROT>(
             p, v, cbase + h * 64, ln, [&](int f) { return bv[h][f]; },
             [&](int k) { return cs[u % (RD + 1)][k]; }, put);
       };
@@ -1454,9 +1044,10 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 #pragma clang diagnostic pop
 
 // ---------------------------------------------------------------------------
-// Tile configurations of the 4-wave kernels, which take what the ping-pong
-// kernel does not (fp32, GELU/tanh epilogues, N % 256 != 0): 16-bit 256x128
-// tiles of 4 waves x (128x64); fp32 128x64 tiles of 2 waves.
+// Tile configurations of the older 4-wave kernels, which take what the
+// persistent four-wave kernel does not (fp32, tanh and reference-formula
+// epilogues, N % 256 != 0, K % 128 != 0): 16-bit 256x128 tiles of 4 waves x
+// (128x64); fp32 128x64 tiles of 2 waves.
 // ---------------------------------------------------------------------------
 struct Cfg256x128 { static constexpr int BM = 256, BN = 128, BK = 64, WM = 2, WN = 2; };
 struct CfgF32 { static constexpr int BM = 128, BN = 64, BK = 32, WM = 2, WN = 1; };
@@ -1486,10 +1077,11 @@ static int cu_count() {
   return counts[dev];
 }
 
-// Epilogues the ping-pong kernel is built for.  The others (GELU, tanh, the
-// reference-formula SiLU) need more registers than it leaves next to its
-// accumulators and take the 4-wave kernels; so does RoPE with a bias.
-constexpr bool pp_epilogue_ok(int epi, int math) {
+// Epilogues the four-wave kernel is built for.  The others (tanh, the
+// reference-formula GELU and SiLU) need more registers than it leaves next to
+// its accumulators and take the older 4-wave kernels; so does RoPE with a
+// bias.
+constexpr bool w4_epilogue_ok(int epi, int math) {
   return epi == EPI_STORE || epi == EPI_ROPE ||
          (math == MATH_EXACT && (epi == EPI_SWIGLU || epi == EPI_GELU));
 }
@@ -1507,18 +1099,6 @@ static int persistent_grid(int ntiles) {
   const int g8 = (grid + 7) / 8 * 8;
   if (g8 <= cus && (ntiles + g8 - 1) / g8 == rounds) grid = g8;
   return grid;
-}
-
-template <typename T, int EPI, int MATH>
-static hipError_t launch_pp(const GemmParams& p, hipStream_t s) {
-  const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
-  const int grid = persistent_grid(ntiles);
-  // SwiGLU's output staging area (8 waves x kPpSpread KB) takes the
-  // LDS of one stage when it exceeds the 32 KB that four stages leave.
-  constexpr int NS = EPI == EPI_SWIGLU && kPpSpread > 4 ? kPpNS - 1 : kPpNS;
-  hipLaunchKernelGGL((gemm_pp_kernel<T, EPI, MATH, kPpBK, NS>), dim3(grid), dim3(512), 0,
-                     s, p, ntiles);
-  return hipGetLastError();
 }
 
 // The four-wave kernel's K loop runs in groups of four steps with at least
@@ -1555,13 +1135,12 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
   if constexpr (sizeof(T) == 4) {
     return launch_cfg<T, CfgF32, EPI, MATH>(p, s);
   } else {
-    // B packed for the ping-pong kernel (gemm_pp_layout) goes there; only the
-    // epilogues it was built for reach this point with such a layout.
+    // B packed for the four-wave kernel (gemm_w4_layout) goes there; only the
+    // epilogues and shapes it was built for reach this point with such a
+    // layout (gemm_nt_supported).
     if (p.epi.layout >= PACK_LANE16) {
-      if constexpr (pp_epilogue_ok(EPI, MATH)) {
+      if constexpr (w4_epilogue_ok(EPI, MATH)) {
         if (gemm_w4_ok(p)) return launch_w4<T, EPI, MATH>(p, s);
-        if (p.epi.out_tiled || p.epi.a_tiled || p.epi.c_padded) return hipErrorInvalidValue;
-        return launch_pp<T, EPI, MATH>(p, s);
       }
       return hipErrorInvalidValue;
     }
@@ -1595,12 +1174,10 @@ static bool cfg_ok(int N, int K) {
   else return N % Cfg256x128::BN == 0 && K % Cfg256x128::BK == 0;
 }
 
-int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
+int gemm_w4_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
   if (dtype != F16 && dtype != BF16) return -1;
-  if (N <= 0 || K <= 0 || N % 256 || K % kPpBK) return -1;
-  if (!pp_epilogue_ok(epi_kind, math)) return -1;
-  // SwiGLU stores a tile's staged row blocks over the next tile's K steps.
-  if (epi_kind == EPI_SWIGLU && K / kPpBK < 8) return -1;
+  if (N <= 0 || N % 256 || !gemm_w4_shape_ok(K)) return -1;
+  if (!w4_epilogue_ok(epi_kind, math)) return -1;
   if (epi_kind == EPI_ROPE) return has_bias ? -1 : PACK_ROPE;
   return epi_kind == EPI_SWIGLU ? PACK_SWIGLU_LANE : PACK_LANE16;
 }
@@ -1608,15 +1185,13 @@ int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bia
 int gemm_padded_width(int dtype, int N, int K, int epi_kind, int math, bool has_bias) {
   if (N <= 0 || N % 256 == 0 || epi_kind == EPI_SWIGLU || epi_kind == EPI_ROPE) return N;
   const int np = (N + 255) / 256 * 256;
-  return gemm_pp_layout(dtype, np, K, epi_kind, math, has_bias) >= 0 && gemm_w4_shape_ok(K) ? np
-                                                                                           : N;
+  return gemm_w4_layout(dtype, np, K, epi_kind, math, has_bias) >= 0 ? np : N;
 }
 
 bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
                    bool a_tiled, bool c_padded) {
   if (!out_tiled && !a_tiled && !c_padded) return true;
-  if (gemm_pp_layout(dtype, N, K, epi_kind, math, has_bias) < 0 || !gemm_w4_shape_ok(K))
-    return false;
+  if (gemm_w4_layout(dtype, N, K, epi_kind, math, has_bias) < 0) return false;
   if (out_tiled && (epi_kind != EPI_SWIGLU || (N / 2) % 32)) return false;
   return true;
 }
@@ -1628,18 +1203,21 @@ bool gemm_nt_supported(int dtype, int M, int N, int K, const void* A, int lda, c
                      epi.a_tiled, epi.c_padded))
     return false;
   if (epi.layout >= PACK_LANE16) {
-    if (gemm_pp_layout(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr) != epi.layout)
+    if (gemm_w4_layout(dtype, N, K, epi.kind, epi.math, epi.bias != nullptr) != epi.layout)
       return false;
     if (lda % 8 || ldb % 8 || ldc % 8) return false;
     if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C | (uintptr_t)epi.bias) & 15) return false;
-    if (epi.kind == EPI_ROPE && (epi.rope_cols % 64 || !epi.pos || !epi.rope_cs)) return false;
+    // The RoPE epilogue gives both 64-feature heads of a wave the same table
+    // and rotation: its column bounds are multiples of 128.
+    if (epi.kind == EPI_ROPE && (epi.rope_cols % 128 || !epi.pos || !epi.rope_cs)) return false;
     if (epi.q_cols && (epi.q_cols % 64 || (epi.kind != EPI_STORE && epi.kind != EPI_ROPE)))
       return false;
-    if (epi.q_cols && epi.kind == EPI_ROPE && (!epi.rope_cs_q || epi.q_cols > epi.rope_cols))
+    if (epi.q_cols && epi.kind == EPI_ROPE &&
+        (epi.q_cols % 128 || !epi.rope_cs_q || epi.q_cols > epi.rope_cols))
       return false;
     return true;
   }
-  if (epi.q_cols) return false;  // only the ping-pong epilogues scale a query block
+  if (epi.q_cols) return false;  // only the four-wave epilogues scale a query block
   if (epi.layout != (epi.kind == EPI_SWIGLU ? PACK_SWIGLU16 : PACK_PLAIN)) return false;
   const int esz = dtype == F32 ? 4 : 2;
   const int epc = 16 / esz;

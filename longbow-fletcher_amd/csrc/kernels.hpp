@@ -19,9 +19,9 @@ enum EpiKind : int {
 
 // Row order of a packed [N, K] weight matrix (and of its fp32 bias): which
 // packed row holds logical output column n.  Within each 64-row block the
-// ping-pong layouts put the columns an MFMA lane accumulates (4 rows of each
-// of 4 16-row tiles) on adjacent outputs, so the epilogue stores 16 bytes per
-// lane:
+// four-wave kernel's layouts put the columns an MFMA lane accumulates (4 rows
+// of each of 4 16-row tiles) on adjacent outputs, so the epilogue produces 16
+// bytes per lane:
 //   PACK_LANE16       lane g holds outputs [16g, 16g+16) of the block
 //   PACK_ROPE         lane g holds [8g, 8g+8) and [32+8g, 32+8g+8) of a
 //                     64-wide head, i.e. both halves of its rotate-half pairs
@@ -59,7 +59,7 @@ __host__ __device__ inline int packed_row(int n, int N, int layout) {
 }
 
 // Element offset of (packed row r, column k) in a packed [N, K] weight
-// matrix.  The ping-pong layouts (16-bit, N % 256 == 0, K % 32 == 0) are
+// matrix.  The four-wave kernel's layouts (16-bit, N % 256 == 0) are
 // stored tiled: block (r / 256, k / 32) is 256 rows x 32 columns, 16 KB,
 // blocks ordered by row tile then K slice; inside a block, row r % 256 is 64
 // bytes whose 16-byte chunk c sits in slot c ^ ((r % 256) >> 1 & 3).  That is
@@ -82,7 +82,7 @@ struct GemmEpilogue {
   int layout = PACK_PLAIN;         // PackLayout of B and bias
   // Output columns [0, q_cols) are multiplied by q_scale last (the query
   // block of a fused QKV projection, pre-scaled for the flash kernel).  The
-  // ping-pong kernel's STORE epilogue multiplies; its RoPE epilogue rotates
+  // four-wave kernel's STORE epilogue multiplies; its RoPE epilogue rotates
   // those columns with rope_cs_q, the table times q_scale.  gemm_nt_supported
   // rejects q_cols elsewhere.
   int q_cols = 0;
@@ -103,22 +103,23 @@ struct GemmEpilogue {
 };
 
 // Element offset of (row m, column k) of an activation matrix with K columns
-// stored tiled: the layout of packed_offset for a ping-pong weight matrix.
+// stored tiled: the layout of packed_offset for a four-wave weight matrix.
 __host__ __device__ inline size_t tiled_act_offset(int64_t m, int k, int K) {
   const int rr = (int)(m % 256), slot = ((k % 32) / 8) ^ ((rr >> 1) & 3);
   return ((size_t)(m / 256) * (K / 32) + k / 32) * 8192 + rr * 32 + slot * 8 + k % 8;
 }
 
 // Whether the tiled-activation options can be used for this GEMM (the
-// four-wave kernel takes it): 16-bit, ping-pong layout, K % 128 == 0,
+// four-wave kernel takes it): 16-bit, a four-wave layout, K % 128 == 0,
 // K >= 256; out_tiled only with the SwiGLU epilogue.
 bool gemm_tiled_ok(int dtype, int N, int K, int epi_kind, int math, bool has_bias, bool out_tiled,
                    bool a_tiled, bool c_padded);
 
-// The packing the ping-pong GEMM needs for this problem, or -1 when that
+// The packing the persistent four-wave GEMM needs for this problem (16-bit,
+// N % 256 == 0, K % 128 == 0, K >= 256, an epilogue it has), or -1 when that
 // kernel does not take it (the caller then packs PACK_PLAIN / PACK_SWIGLU16
-// for the 4-wave kernels).
-int gemm_pp_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias);
+// for the older 4-wave kernels).
+int gemm_w4_layout(int dtype, int N, int K, int epi_kind, int math, bool has_bias);
 
 // The output width a model uses for a 16-bit projection of N outputs: N, or
 // the next multiple of 256 when the four-wave kernel takes that width and N

@@ -630,7 +630,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     const bool has_bias = c.has_bias != 0;
     auto pick = [&](bool mfma, int N, int K, int kind, int fallback) {
       if (!mfma) return (int)PACK_PLAIN;
-      const int l = gemm_pp_layout(m->dtype, N, K, kind, c.math, has_bias);
+      const int l = gemm_w4_layout(m->dtype, N, K, kind, c.math, has_bias);
       return l >= 0 ? l : fallback;
     };
     m->lay_qkv = pick(m->mfma_qkv, m->Nqkv, m->H,
@@ -641,7 +641,7 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
     if (m->swiglu && !m->mfma_up) m->lay_up = PACK_PLAIN;
     m->lay_down = pick(m->mfma_down, m->Nh, m->I, EPI_STORE, PACK_PLAIN);
     // The flash kernel takes Q pre-scaled when the QKV projection runs on the
-    // ping-pong kernel, whose epilogue applies the scale.
+    // four-wave kernel, whose epilogue applies the scale.
     m->q_prescaled = m->hd == 64 && m->dtype != FL_F32 && m->lay_qkv >= PACK_LANE16 &&
                      m->H % 64 == 0;
     m->ffn_tiled = m->swiglu && m->lay_up == PACK_SWIGLU_LANE && m->lay_down >= PACK_LANE16 &&

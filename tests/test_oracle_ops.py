@@ -4,6 +4,7 @@ mathematical invariants of each op."""
 import json
 import math
 import pathlib
+import zlib
 
 import numpy as np
 import pytest
@@ -11,6 +12,14 @@ import pytest
 KNOWN = json.loads((pathlib.Path(__file__).parent / "golden" /
                     "reference_known_answers.json").read_text())
 RNG = np.random.default_rng(11)
+
+
+@pytest.fixture(autouse=True)
+def _inputs_per_test(request):
+    """Each test draws its random inputs from a seed of its own (derived from
+    its name), so they do not depend on which tests ran before it."""
+    global RNG
+    RNG = np.random.default_rng([11, zlib.crc32(request.node.name.encode())])
 
 
 def rand(*shape, scale=1.0):
