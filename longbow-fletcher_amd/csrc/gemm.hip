@@ -908,6 +908,16 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       block(I0{});
       block(I1{});
     };
+    // The QKV (RoPE) and SwiGLU outputs are written as non-temporal stores:
+    // at the encoder's sizes they are larger than the caches and the next
+    // kernel reads them from the start, so the cached copies would only
+    // evict data read again sooner (measured: QKV GEMM -3%, attention -4%,
+    // FFN-up -1.4%).
+    constexpr bool NTS = EPI == EPI_ROPE || EPI == EPI_SWIGLU;
+    auto put16 = [&](T* dst, u32x4_t val) __attribute__((always_inline)) {
+      if constexpr (NTS) __builtin_nontemporal_store(val, (u32x4_t*)dst);
+      else *(u32x4_t*)dst = val;
+    };
     auto store_unit = [&](auto uc, auto rotc) __attribute__((always_inline)) {
       constexpr int u = decltype(uc)::value;
       constexpr int t = u;
@@ -924,7 +934,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
             const int cc = kk * 4 + (slot ^ ((rr >> 1) & 3));
             const u32x4_t val = *(const u32x4_t*)(buf + rr * RB + ((cc ^ (rr % CPRW)) << 4));
             const size_t blk = (size_t)(m0 / 256) * (p.ldc / 32) + col0 / 32 + kk;
-            *(u32x4_t*)((T*)p.C + blk * 8192 + trow * 32 + ln * 8) = val;
+            put16((T*)p.C + blk * 8192 + trow * 32 + ln * 8, val);
           }
           return;
         }
@@ -938,7 +948,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
         // row M-1's outputs (computed from its inputs) and are stored there
         // again: the same bytes.  Either way, no branch.
         const int m = min(m0 + wm * 128 + t * 16 + rr, mlast);
-        *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + col0 + c * 8) = val;
+        put16((T*)p.C + (size_t)m * p.ldc + col0 + c * 8, val);
       }
     };
     if constexpr (EPI == EPI_ROPE) {

@@ -35,6 +35,21 @@ __device__ inline void load_vec(const T* p, float* out) {
   }
 }
 
+// load_vec for data read once: 16-bit 8-vectors go out as non-temporal
+// loads, which leave the caches to the data read again later (the residual
+// stream the LayerNorm writes and the next kernels read).
+template <typename T, int VEC>
+__device__ inline void load_vec_once(const T* p, float* out) {
+  if constexpr (VEC == 8 && sizeof(T) == 2) {
+    using V8 = T __attribute__((ext_vector_type(8)));
+    const V8 v = __builtin_nontemporal_load((const V8*)p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = to_f(v[i]);
+  } else {
+    load_vec<T, VEC>(p, out);
+  }
+}
+
 template <typename T, int VEC>
 __device__ inline void store_vec(T* p, const float* in) {
   if constexpr (VEC == 8 && sizeof(T) == 2) {
@@ -160,11 +175,12 @@ layernorm_rows_kernel(T* t, const T* residual, int ldr, int rows, int cols, cons
     if (valid[c]) load_vec<T, VEC>(tp(col0[c]), x[c]);
   }
   if (rr) {
+    // The residual branch (a GEMM output) is dead after this kernel.
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
       if (valid[c]) {
         float r[VEC];
-        load_vec<T, VEC>(rr + col0[c], r);
+        load_vec_once<T, VEC>(rr + col0[c], r);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + r[i];
       }
