@@ -516,11 +516,6 @@ __device__ inline u32x4_t pack8(float4_t a, float4_t b) {
   }
 }
 
-template <typename T>
-__device__ inline void store8(T* dst, float4_t a, float4_t b) {
-  *(u32x4_t*)dst = pack8<T>(a, b);
-}
-
 // One 16-row block of a 64-feature group: v[f] is accumulator tile f of the
 // group for the lane's token row; nbase is the group's first (packed) output
 // column.  bias_at(f) gives the bias of tile f (added when BIAS), rope_at(k)
