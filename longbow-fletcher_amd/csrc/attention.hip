@@ -101,8 +101,11 @@ __device__ __attribute__((always_inline)) inline void attn_dma(uint32_t lds_dst,
 // scale * log2(e) (the encoder's QKV epilogue does it), so the first score
 // MFMA starts from the accumulator -m and produces x directly; otherwise x
 // takes one FMA per score.
+// The four-wave form asks for four waves per SIMD (at most 128 VGPRs): with
+// only the block size to go by, the register allocator may pick 130.
 template <typename T, int D, int WAVES, bool PRE>
-__global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
+__global__ void __launch_bounds__(WAVES * 64)
+    __attribute__((amdgpu_waves_per_eu(WAVES == 4 ? 4 : 1))) attn_flash_kernel(AttnParams p) {
   static_assert(D == 32 || D == 64, "head size 32 or 64");
   constexpr int BKV = 64, NT = WAVES * 64;
   constexpr int ROWB = D * 2;           // bytes of one key / value row of a head
@@ -363,20 +366,37 @@ __global__ void __launch_bounds__(WAVES * 64) attn_flash_kernel(AttnParams p) {
     if (it + 1 < ntiles) tile(it + 1, std::integral_constant<int, 1>{});
   }
 
+  // The output goes through LDS, each wave's 32 rows in an area of its own
+  // (every wave has passed the last tile's barrier, so the K/V buffers are
+  // free), to leave as 16-byte stores of whole rows instead of 8-byte pieces
+  // of 16 rows.  Chunk c of row r sits at chunk c ^ (r % CH).
   T* out = (T*)p.out;
+  char* ost = &lds[0][0][0] + wave * 32 * ROWB;
+  // An opaque copy of the lane id keeps the stores' address arithmetic from
+  // being hoisted into the key loop, where it would hold registers.
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int olr = ln & 15, og = ln >> 4;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const float inv = 1.0f / lacc[qt][0];
-    const int qr = qbase + qt * 16 + lr;
-    if (qr >= L) continue;
-    T* orow = out + (size_t)(s0 + qr) * p.ldo + hoff + g * 4;
+    const int row = qt * 16 + olr;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       V4 h;
 #pragma unroll
       for (int i = 0; i < 4; ++i) h[i] = (T)(o[dt][qt][i] * inv);
-      *(V4*)(orow + dt * 16) = h;
+      const int c = dt * 2 + (og >> 1);
+      *(V4*)(ost + row * ROWB + ((c ^ (row & (CH - 1))) << 4) + (og & 1) * 8) = h;
     }
+  }
+  constexpr int RPR = 64 / CH;  // rows per 64 lanes x 16 bytes
+#pragma unroll
+  for (int k = 0; k < 32 / RPR; ++k) {
+    const int row = k * RPR + ln / CH, c = ln % CH;
+    const u32x4_t val = *(const u32x4_t*)(ost + row * ROWB + ((c ^ (row & (CH - 1))) << 4));
+    const int qr = qbase + row;
+    if (qr < L) *(u32x4_t*)(out + (size_t)(s0 + qr) * p.ldo + hoff + c * 8) = val;
   }
 }
 
