@@ -319,6 +319,56 @@ embed_ln_kernel(const int* ids, const int* pos_ids, const T* word, const T* pos_
                         x[c]);
 }
 
+// The same with 16-byte vectors and LPR lanes per row (64 / LPR rows per
+// wave), for 16-bit widths of 32*8 .. 4*32*8: the rows of a wave are
+// adjacent, so with the tiled output each store of the wave writes whole
+// 128-byte lines (two rows' 64-byte pieces of a K slice) instead of halves.
+template <typename T, int LPR, int NCH, bool OT>
+__global__ void __launch_bounds__(256)
+embed_rows_kernel(const int* ids, const int* pos_ids, const T* word, const T* pos_table,
+                  const T* type_table, int rows, int cols, const float* gamma,
+                  const float* beta, float eps, int vocab, int* bad_id, T* out) {
+#pragma clang fp contract(off)
+  constexpr int VEC = 8, RPW = 64 / LPR;
+  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + ((threadIdx.x & 63) / LPR);
+  const int lane = threadIdx.x % LPR;
+  if (row >= rows) return;
+  int id = ids[row];
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(bad_id, 1);
+    id = 0;
+  }
+  const T* wr = word + (size_t)id * cols;
+  const T* pr = pos_table ? pos_table + (size_t)pos_ids[row] * cols : nullptr;
+  float x[NCH][VEC];
+  bool valid[NCH];
+  int col0[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    col0[c] = (lane + c * LPR) * VEC;
+    valid[c] = col0[c] < cols;
+    if (valid[c]) {
+      load_vec<T, VEC>(wr + col0[c], x[c]);
+      float y[VEC];
+      if (pr) {
+        load_vec<T, VEC>(pr + col0[c], y);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + y[i];
+      }
+      load_vec<T, VEC>(type_table + col0[c], y);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + y[i];
+    }
+  }
+  ln_core<NCH, VEC, LPR>(x, valid, cols, gamma, beta, col0, eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (valid[c])
+      store_vec<T, VEC>(OT ? out + tiled_act_offset(row, col0[c], cols)
+                           : out + (size_t)row * cols + col0[c],
+                        x[c]);
+}
+
 struct EmbArgs {
   const int* ids;
   const int* pos_ids;
@@ -350,8 +400,34 @@ static hipError_t emb_launch(const EmbArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <typename T, int NCH>
+static hipError_t emb_rows_launch(const EmbArgs& a, hipStream_t s) {
+  constexpr int rows_per_block = 4 * (64 / 32);
+  const dim3 grid((a.T + rows_per_block - 1) / rows_per_block);
+  if (a.out_tiled)
+    hipLaunchKernelGGL((embed_rows_kernel<T, 32, NCH, true>), grid, dim3(256), 0, s, a.ids,
+                       a.pos_ids, (const T*)a.word, (const T*)a.pos_table,
+                       (const T*)a.type_table, a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id,
+                       (T*)a.out);
+  else
+    hipLaunchKernelGGL((embed_rows_kernel<T, 32, NCH, false>), grid, dim3(256), 0, s, a.ids,
+                       a.pos_ids, (const T*)a.word, (const T*)a.pos_table,
+                       (const T*)a.type_table, a.T, a.H, a.g, a.b, a.eps, a.vocab, a.bad_id,
+                       (T*)a.out);
+  return hipGetLastError();
+}
+
 template <typename T>
 static hipError_t emb_typed(const EmbArgs& a, hipStream_t s) {
+  // 16-bit rows of 256 .. 1024 elements: 32 lanes per row, 16-byte vectors.
+  if (sizeof(T) == 2 && a.H % 256 == 0 && a.H <= 1024) {
+    switch (a.H / 256) {
+      case 1: return emb_rows_launch<T, 1>(a, s);
+      case 2: return emb_rows_launch<T, 2>(a, s);
+      case 3: return emb_rows_launch<T, 3>(a, s);
+      case 4: return emb_rows_launch<T, 4>(a, s);
+    }
+  }
   if (a.H % 4 == 0) {
     const int nch = (a.H / 4 + 63) / 64;
     if (nch <= 1) return emb_launch<T, 1, 4>(a, s);
