@@ -106,7 +106,7 @@ def counters_summary(fetch_dir, write_dir, workload, out_path):
                 # (weight loading runs cast_kernel<fp32, fp16> before it).
                 calib = val
                 continue
-            if "embed_ln" in name:
+            if "embed_ln" in name or "embed_rows" in name:
                 cls = "embed"
             elif "attn_" in name:
                 cls = "attention"
@@ -114,7 +114,7 @@ def counters_summary(fetch_dir, write_dir, workload, out_path):
                 cls = "add_layernorm"
             elif "pool_" in name:
                 cls = "pool"
-            elif "gemm_w4" in name or "gemm_pp" in name:
+            elif "gemm_w4" in name:
                 epi = name.split("kernelIDF16_Li")[1][0] if "kernelIDF16_Li" in name else "?"
                 if epi == "4":
                     cls = "qkv_gemm"
