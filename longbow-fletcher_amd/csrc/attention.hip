@@ -34,6 +34,10 @@ struct AttnParams {
   const AttnWork* work;
   float scale;
   int group;  // consecutive work items per XCD (query blocks of one sequence-head)
+  // > 0: the output is stored in the tiled activation layout
+  // (tiled_act_offset) with this many columns, for a GEMM that reads it as a
+  // tiled operand; ldo is then unused.
+  int out_tiled_cols;
 };
 
 template <typename T> struct AttnMfma;
@@ -390,6 +394,23 @@ __global__ void __launch_bounds__(WAVES * 64)
       *(V4*)(ost + row * ROWB + ((c ^ (row & (CH - 1))) << 4) + (og & 1) * 8) = h;
     }
   }
+  if (p.out_tiled_cols > 0) {
+    // Tiled output: the 16-row halves of each 32-column slice of the head
+    // are contiguous 1 KB blocks (rows of one 256-row tile); lane l writes
+    // 16-byte chunk l % 4 of row l / 4.
+#pragma unroll
+    for (int sl = 0; sl < D / 32; ++sl)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = j * 16 + (ln >> 2), c = sl * 4 + (ln & 3);
+        const u32x4_t val =
+            *(const u32x4_t*)(ost + row * ROWB + ((c ^ (row & (CH - 1))) << 4));
+        const int qr = qbase + row;
+        if (qr < L)
+          *(u32x4_t*)(out + tiled_act_offset(s0 + qr, hoff + c * 8, p.out_tiled_cols)) = val;
+      }
+    return;
+  }
   constexpr int RPR = 64 / CH;  // rows per 64 lanes x 16 bytes
 #pragma unroll
   for (int k = 0; k < 32 / RPR; ++k) {
@@ -421,12 +442,13 @@ hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
                                   const AttnWork* work, int n_work, int head_dim, float scale,
                                   int waves, bool q_prescaled, int xcd_group_size,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, int out_tiled_cols) {
   if (n_work <= 0) return hipSuccess;
+  if (out_tiled_cols && (out_tiled_cols % 32 || head_dim != 64)) return hipErrorInvalidValue;
   if ((head_dim != 32 && head_dim != 64) || (head_dim == 32 && q_prescaled))
     return hipErrorInvalidValue;
   const AttnParams p{q, k, v, out, ldqkv, ldo, cu_seqlens, work, scale,
-                     std::max(1, std::min(xcd_group_size, 32))};
+                     std::max(1, std::min(xcd_group_size, 32)), out_tiled_cols};
   if (dtype == F16) launch_flash_typed<_Float16>(p, n_work, head_dim, waves, q_prescaled, stream);
   else if (dtype == BF16) launch_flash_typed<__bf16>(p, n_work, head_dim, waves, q_prescaled, stream);
   else return hipErrorInvalidValue;

@@ -171,11 +171,13 @@ struct AttnWork {
 // types.  q_prescaled (head_dim 64 only): Q already holds q * scale * log2(e)
 // (GemmEpilogue::q_scale).  xcd_group_size: consecutive work items (the query
 // blocks of one sequence and head) kept on one XCD, clamped to [1, 32].
+// out_tiled_cols > 0 (head size 64): out is written in the tiled activation
+// layout (tiled_act_offset) with that many columns instead of row-major.
 hipError_t launch_attention_flash(int dtype, const void* q, const void* k, const void* v,
                                   int ldqkv, void* out, int ldo, const int* cu_seqlens,
                                   const AttnWork* work, int n_work, int head_dim, float scale,
                                   int waves, bool q_prescaled, int xcd_group_size,
-                                  hipStream_t stream);
+                                  hipStream_t stream, int out_tiled_cols = 0);
 // Two-pass attention (exact row max, then reference ExpFast or exp) for
 // head_dim 64 fp32.
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v, int ldqkv,

@@ -154,6 +154,9 @@ struct fl_model {
   // activations) is kept tiled too; activation buffers then have rows up to
   // a multiple of 256 and the GEMMs reading X write their padding rows.
   bool x_tiled = false;
+  // The attention output CTX (the O projection's activations) is kept tiled
+  // as well, so the O projection streams it in contiguous 16 KB blocks.
+  bool ctx_tiled = false;
 
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;
@@ -482,7 +485,8 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
       // faster than one pair at 512 tokens (the kernel clamps groups at 32).
       if ((m->hd == 64 || m->hd == 32) && dt != FL_F32)
         M_CHECK(launch_attention_flash(dt, q, k, v, m->Nqkv, L.CTX, H, L.cu, L.work, L.n_work,
-                                       m->hd, scale, L.waves, m->q_prescaled, 2 * L.qblocks, s));
+                                       m->hd, scale, L.waves, m->q_prescaled, 2 * L.qblocks, s,
+                                       m->ctx_tiled ? H : 0));
       else if (m->hd == 64)
         M_CHECK(launch_attention_f32((const float*)q, (const float*)k, (const float*)v, m->Nqkv,
                                      (float*)L.CTX, H, L.cu, L.work, L.n_work, scale,
@@ -496,6 +500,9 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
       GemmEpilogue e;
       e.bias = m->cfg.has_bias ? w.bo : nullptr;
       e.layout = m->lay_o;
+      // A tiled CTX has rows up to the next 256 that the attention never
+      // writes: O writes their (meaningless) outputs to TMP's own padding rows.
+      e.a_tiled = e.c_padded = m->ctx_tiled;
       M_ST(gemm(m, L, m->mfma_o, L.CTX, w.wo, L.TMP, Ti, m->Nh, H, e));
     }
     {
@@ -655,6 +662,10 @@ int fl_model_create(fl_context* ctx, const fl_model_config* cfg, fl_model** out)
                                true) &&
                  gemm_tiled_ok(m->dtype, m->Ni, m->H, EPI_SWIGLU, c.math, has_bias, true, true,
                                false);
+    // The flash kernel writes CTX tiled for head size 64 (the 16-bit path).
+    m->ctx_tiled = m->x_tiled && m->hd == 64 && m->mfma_o && m->lay_o >= PACK_LANE16 &&
+                   gemm_tiled_ok(m->dtype, m->Nh, m->H, EPI_STORE, c.math, has_bias, false, true,
+                                 true);
   }
 
   auto fill_f32 = [&](float** dst, size_t n, float v) -> int {
