@@ -140,15 +140,17 @@ __global__ void __launch_bounds__(WAVES * 64)
   // Q fragments: [q-tile][d-slice]; lane holds 8 consecutive d of one query.
   const int qbase = w.q0 + wave * 32;
   u32x4_t qf[2][DS];
+  if constexpr (D != 64) {
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qr = qbase + qt * 16 + lr;
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qr = qbase + qt * 16 + lr;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      if (qr < L)
-        qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + g * 8);
-      else
-        qf[qt][ds] = u32x4_t{0, 0, 0, 0};
+      for (int ds = 0; ds < DS; ++ds) {
+        if (qr < L)
+          qf[qt][ds] = *(const u32x4_t*)(Q + (size_t)(s0 + qr) * p.ld + hoff + ds * 32 + g * 8);
+        else
+          qf[qt][ds] = u32x4_t{0, 0, 0, 0};
+      }
     }
   }
 
@@ -362,8 +364,38 @@ __global__ void __launch_bounds__(WAVES * 64)
     __syncthreads();
   };
 
+  // Head size 64: the wave's 32 Q rows come by DMA as whole 128-byte rows
+  // into the four 1 KB blocks of buffer 1 that its own loads of tile 1 fill
+  // later (K and V blocks wave and 4 + wave), chunk c of row r at slot
+  // c ^ (r % 8); rows past the sequence re-read its last row.
+  const lds_char* qlds[4] = {(const lds_char*)lds[1][0] + wave * 1024,
+                             (const lds_char*)lds[1][0] + (4 + wave) * 1024,
+                             (const lds_char*)lds[1][1] + wave * 1024,
+                             (const lds_char*)lds[1][1] + (4 + wave) * 1024};
+  if constexpr (D == 64) {
+    const char* qseq = (const char*)(Q + (size_t)s0 * ldk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = i * 8 + (lane >> 3);
+      const int qr = min(qbase + row, L - 1);
+      const uint32_t qo =
+          (uint32_t)(((size_t)qr * ldk + hoff + (((lane & 7) ^ (row & 7)) << 3)) * sizeof(T));
+      attn_dma((uint32_t)(uintptr_t)qlds[i], qo, qseq);
+    }
+  }
   issue(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (D == 64) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int row = qt * 16 + lr;
+      const lds_char* rb = qlds[2 * qt + (lr >> 3)] + (row & 7) * 128;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        qf[qt][ds] = *(const __attribute__((address_space(3))) u32x4_t*)(
+            rb + ((((ds * 4 + g) ^ (row & 7))) << 4));
+    }
+  }
   __syncthreads();
   for (int it = 0; it < ntiles; it += 2) {
     tile(it, std::integral_constant<int, 0>{});
