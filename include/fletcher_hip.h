@@ -298,15 +298,19 @@ int fl_model_forward_device(fl_model *model, const int32_t *d_ids, const int64_t
  * sequences are taken in order into batches that end before the sequence
  * that would pass max_seqs sequences or max_tokens tokens (a batch always
  * holds at least one; the reference's Linux GPU defaults are 512 and 16384,
- * embeddings.go:84-131), and each batch runs the model forward.  Consecutive
- * batches run on three streams at once, each carrying its batch's id upload,
- * forward and vector download, replacing the reference's double-buffered
- * outputs (:766-775).
+ * embeddings.go:84-131).  Consecutive batches of that plan are computed
+ * together, in forwards of up to 65536 tokens (a larger batch alone): a
+ * sequence's vector does not depend on the other sequences of its forward,
+ * so every output bit is what one forward per batch gives.  Consecutive
+ * forwards run on three streams at once, each carrying its forward's id
+ * upload, kernels and vector download, replacing the reference's
+ * double-buffered outputs (:766-775).
  * ids: flat host ids of all sequences (framing included, as in
  * fl_model_forward); out: host fp32 [nseq x hidden] in input order;
  * batch_nan (optional) int32 [nseq]: 1 where the sequence's batch output held
  * a NaN/Inf (the per-batch HasNaN check, :757-764); nbatches (optional): the
- * number of batches run.  Returns when every output is on the host. */
+ * number of batches of the plan.  Returns when every output is on the host;
+ * fl_model_status then reports the plan's last batch. */
 int fl_model_embed(fl_model *model, const int64_t *ids, const int64_t *lengths, int nseq,
                    int max_seqs, int64_t max_tokens, float *out, int32_t *batch_nan,
                    int *nbatches);

@@ -127,6 +127,18 @@ __global__ void has_nan_kernel(const T* t, int64_t n, int* flag) {
   if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
 }
 
+// One wave per row of an fp32 [rows x cols] matrix: flags[r] = 1 if row r
+// holds a NaN or an infinity, else 0 (every row's flag is written).
+__global__ void row_nonfinite_kernel(const float* t, int rows, int cols, int* flags) {
+  const int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (r >= rows) return;  // uniform per wave
+  const float* row = t + (size_t)r * cols;
+  bool bad = false;
+  for (int c = threadIdx.x & 63; c < cols; c += 64) bad |= !isfinite(row[c]);
+  const bool any = __any(bad);
+  if ((threadIdx.x & 63) == 0) flags[r] = any ? 1 : 0;
+}
+
 template <typename T>
 __global__ void gather_kernel(const T* table, int cols, const int* idx, int n, T* out) {
   const int64_t total = (int64_t)n * cols;
@@ -428,6 +440,13 @@ hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStr
   if (n <= 0) return hipSuccess;
   FL_DISPATCH(dtype, T, hipLaunchKernelGGL(has_nan_kernel<T>, grid_for(n), dim3(256), 0, s,
                                            (const T*)t, n, flag));
+  return hipGetLastError();
+}
+
+hipError_t launch_row_nonfinite(const float* t, int rows, int cols, int* flags, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(row_nonfinite_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, t, rows, cols,
+                     flags);
   return hipGetLastError();
 }
 

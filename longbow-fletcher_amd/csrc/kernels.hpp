@@ -214,6 +214,8 @@ hipError_t launch_activation(int dtype, void* t, int rows, int cols, int act, in
 hipError_t launch_cast(const void* src, int sdt, void* dst, int ddt, int64_t n, int truncate_ref,
                        hipStream_t s);
 hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStream_t s);
+// flags[r] = 1 if row r of fp32 t [rows x cols] holds a NaN or an infinity, else 0.
+hipError_t launch_row_nonfinite(const float* t, int rows, int cols, int* flags, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* table, int cols, const int* idx, int n,
                          void* out, hipStream_t s);
 hipError_t launch_slice(int dtype, const void* src, int cols, int r0, int r1, int c0, int c1,

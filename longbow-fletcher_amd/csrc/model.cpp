@@ -59,13 +59,23 @@ struct Staging {
 // activation buffers, the batch metadata and the stream the forward runs on.
 // Lane 0 runs on the context stream and serves every entry point; the
 // batching loop of fl_model_embed also uses lanes 1 .. kLanes-1, each on a
-// stream of its own, so consecutive batches run concurrently and one batch's
-// kernels fill the CUs the others' leave idle (a 16384-token batch gives its
-// N = 768 GEMMs 192 tiles for 256 CUs).  Three lanes (three of the four
-// hardware queues a process gets) measured best: two leave the device idle
-// while the host prepares the next batch, four gain nothing.
+// stream of its own, so consecutive forwards run concurrently and one
+// forward's kernels fill the CUs the others' leave idle.  Three lanes (three
+// of the four hardware queues a process gets) measured best with
+// 16384-token forwards: two left the device idle while the host prepared the
+// next forward, four gained nothing.
 // Lanes of fl_model_embed's batch pipeline (lane 0 is the context stream's).
 constexpr int kLanes = 3;
+// fl_model_embed computes consecutive batches of its plan together, in
+// forwards of up to this many tokens (a batch larger than that alone).  A
+// sequence's vector does not depend on the other sequences of its forward,
+// so the grouping changes no output bit; it only gives the GEMMs more rows:
+// 16384-token forwards leave the N = 768 GEMMs 192 tiles for 256 CUs.
+// Measured end to end (the whole call, PCIe included) against one forward per
+// batch of the reference's 16384-token plan: config 3 +8%, the ragged batch
+// +9%, BERT-base +4%; one 131072-token forward is no faster than two of
+// 65536 tokens on two lanes.
+constexpr int64_t kGroupTokens = 65536;
 
 struct Lane {
   hipStream_t stream = nullptr;
@@ -130,16 +140,18 @@ struct fl_model {
   // Lane 0: the context stream; lanes 1 .. kLanes-1: fl_model_embed's own.
   Lane lane[kLanes];
 
-  // fl_model_embed's pipeline: ids go up on `up`, pooled vectors and the
-  // batch's flags come back on `down`, forwards run on the lanes' streams.
+  // fl_model_embed's pipeline: one slot per lane; a lane's stream carries
+  // its forward's id upload, the forward and the copies back.
   struct Pipe {
     int32_t* ids_pin[kLanes] = {};
     float* out_pin[kLanes] = {};
     int* flags_pin[kLanes] = {};
+    int* rows_pin[kLanes] = {};   // per-sequence NaN/Inf flags of the forward's output
     int* ids_dev[kLanes] = {};
     float* out_dev[kLanes] = {};
-    uint16_t* out16_dev[kLanes] = {};  // fp16 output of the batch (FL_F16)
+    uint16_t* out16_dev[kLanes] = {};  // fp16 output of the forward (FL_F16)
     int* flags_dev[kLanes] = {};
+    int* rows_dev[kLanes] = {};
     hipEvent_t d2h[kLanes] = {};
     bool ready = false;  // streams and events created
     int64_t cap_tok = 0;
@@ -723,7 +735,8 @@ int fl_model_free(fl_model* m) {
     for (int k = 1; k < kLanes; ++k)
       if (m->lane[k].stream) (void)hipStreamSynchronize(m->lane[k].stream);
     for (int k = 0; k < kLanes; ++k) {
-      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
+      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k],
+                      (void*)P.rows_pin[k]})
         if (h) (void)hipHostFree(h);
       if (P.d2h[k]) (void)hipEventDestroy(P.d2h[k]);
     }
@@ -957,8 +970,7 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
   // always holds at least one sequence.
   struct Batch { int first, count; int64_t tok0, tokens; };
   std::vector<Batch> plan;
-  int64_t tok = 0, max_bt = 0;
-  int max_bs = 0;
+  int64_t tok = 0;
   for (int i = 0; i < nseq;) {
     int count = 0;
     int64_t tokens = 0;
@@ -974,14 +986,32 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
       tokens = lengths[i];
     }
     plan.push_back({i, count, tok, tokens});
-    max_bt = std::max(max_bt, tokens);
-    max_bs = std::max(max_bs, count);
     tok += tokens;
     i += count;
   }
   for (int64_t t = 0; t < tok; ++t)
     if (ids[t] < 0 || ids[t] >= m->cfg.vocab_size)  // cpu_backend.go:500-502
       return fail(FL_ERR_INVALID, "Gather index out of bounds");
+  // Forwards: runs of consecutive batches of at most kGroupTokens tokens
+  // (at least one batch each).
+  struct Group { int b0, nb; };
+  std::vector<Group> groups;
+  int64_t max_gt = 0;
+  int max_gs = 0;
+  for (int b = 0; b < (int)plan.size();) {
+    Group g{b, 0};
+    int64_t gt = 0;
+    int gs = 0;
+    while (b < (int)plan.size() && (g.nb == 0 || gt + plan[(size_t)b].tokens <= kGroupTokens)) {
+      gt += plan[(size_t)b].tokens;
+      gs += plan[(size_t)b].count;
+      ++g.nb;
+      ++b;
+    }
+    groups.push_back(g);
+    max_gt = std::max(max_gt, gt);
+    max_gs = std::max(max_gs, gs);
+  }
 
   fl_model::Pipe& P = m->pipe;
   Lane& L0 = lane0(m);
@@ -994,20 +1024,23 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
       if (!P.d2h[k]) M_CHECK(hipEventCreateWithFlags(&P.d2h[k], hipEventDisableTiming));
     P.ready = true;
   }
-  if (max_bt > P.cap_tok || max_bs > P.cap_seq) {
+  if (max_gt > P.cap_tok || max_gs > P.cap_seq) {
     for (int k = 0; k < kLanes; ++k) M_CHECK(hipStreamSynchronize(m->lane[k].stream));
-    const int64_t ct = std::max(max_bt, P.cap_tok);
-    const int cq = std::max(max_bs, P.cap_seq);
+    const int64_t ct = std::max(max_gt, P.cap_tok);
+    const int cq = std::max(max_gs, P.cap_seq);
     for (int k = 0; k < kLanes; ++k) {
-      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k]})
+      for (void* h : {(void*)P.ids_pin[k], (void*)P.out_pin[k], (void*)P.flags_pin[k],
+                      (void*)P.rows_pin[k]})
         if (h) M_CHECK(hipHostFree(h));
       P.ids_pin[k] = nullptr;
       P.out_pin[k] = nullptr;
       P.flags_pin[k] = nullptr;
+      P.rows_pin[k] = nullptr;
       untrack_free(m, P.ids_dev[k]);
       untrack_free(m, P.out_dev[k]);
       untrack_free(m, P.out16_dev[k]);
       untrack_free(m, P.flags_dev[k]);
+      untrack_free(m, P.rows_dev[k]);
     }
     // Capacities stay 0 until every buffer of every slot exists: a failure
     // here leaves null pointers and the next call reallocates.
@@ -1015,62 +1048,97 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     for (int k = 0; k < kLanes; ++k) {
       if (hipHostMalloc((void**)&P.ids_pin[k], (size_t)ct * 4, hipHostMallocDefault) != hipSuccess ||
           hipHostMalloc((void**)&P.out_pin[k], (size_t)cq * m->H * 4, hipHostMallocDefault) != hipSuccess ||
-          hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess)
+          hipHostMalloc((void**)&P.flags_pin[k], 8, hipHostMallocDefault) != hipSuccess ||
+          hipHostMalloc((void**)&P.rows_pin[k], (size_t)cq * 4, hipHostMallocDefault) != hipSuccess)
         return fail(FL_ERR_OOM, "hipHostMalloc(embed pipeline)");
       M_ST(track_alloc(m, (size_t)ct * 4, P.ids_dev[k]));
       M_ST(track_alloc(m, (size_t)cq * m->H * 4, P.out_dev[k]));
       M_ST(track_alloc(m, (size_t)cq * m->H * 2, P.out16_dev[k]));
       M_ST(track_alloc(m, 8, P.flags_dev[k]));
+      M_ST(track_alloc(m, (size_t)cq * 4, P.rows_dev[k]));
     }
     P.cap_tok = ct;
     P.cap_seq = cq;
   }
 
-  // Batch b uses slot and lane b % kLanes: consecutive batches compute on
+  // Forward f uses slot and lane f % kLanes: consecutive forwards compute on
   // the lanes' streams at the same time, each filling the CUs the others'
-  // kernels leave idle.  A lane's stream carries its batch's upload, forward
-  // and download in order.  The host fills a slot's pinned ids only after
-  // that slot's previous batch has been copied back, and copies results out
-  // of it at the same point: the host runs up to kLanes batches ahead of the
-  // device, like the reference's double buffering of outputs
+  // kernels leave idle.  A lane's stream carries its forward's upload,
+  // kernels and download in order.  The host fills a slot's pinned ids only
+  // after that slot's previous forward has been copied back, and copies
+  // results out of it at the same point: the host runs up to kLanes forwards
+  // ahead of the device, like the reference's double buffering of outputs
   // (embeddings.go:766-775) with one more buffer.
   const int64_t H = m->H;
   const size_t osz = out_dtype == FL_F16 ? 2 : 4;
-  auto drain = [&](int b) -> int {
-    const Batch& pb = plan[(size_t)b];
-    const int k = b % kLanes;
+  // A batch's NaN flag (embeddings.go:757-764: HasNaN on the batch's pooled
+  // output): the forward's own flag when it is one batch, else the OR of
+  // its sequences' row flags.
+  auto batch_flag = [&](const Group& g, int b, int k) -> int {
+    if (g.nb == 1) return P.flags_pin[k][0] != 0;
+    const int r0 = plan[(size_t)b].first - plan[(size_t)g.b0].first;
+    int any = 0;
+    for (int i = 0; i < plan[(size_t)b].count; ++i) any |= P.rows_pin[k][r0 + i];
+    return any != 0;
+  };
+  auto drain = [&](int f) -> int {
+    const Group& g = groups[(size_t)f];
+    const Batch& p0 = plan[(size_t)g.b0];
+    const Batch& pl = plan[(size_t)(g.b0 + g.nb - 1)];
+    const int k = f % kLanes;
     M_CHECK(hipEventSynchronize(P.d2h[k]));
-    std::memcpy((char*)out + (size_t)pb.first * H * osz, P.out_pin[k], (size_t)pb.count * H * osz);
+    std::memcpy((char*)out + (size_t)p0.first * H * osz, P.out_pin[k],
+                (size_t)(pl.first + pl.count - p0.first) * H * osz);
     if (batch_nan)
-      for (int i = 0; i < pb.count; ++i) batch_nan[pb.first + i] = P.flags_pin[k][0] != 0;
+      for (int b = g.b0; b < g.b0 + g.nb; ++b) {
+        const int flag = batch_flag(g, b, k);
+        for (int i = 0; i < plan[(size_t)b].count; ++i) batch_nan[plan[(size_t)b].first + i] = flag;
+      }
     return FL_OK;
   };
-  const int nb = (int)plan.size();
-  for (int b = 0; b < nb; ++b) {
-    const Batch& pb = plan[(size_t)b];
-    const int k = b % kLanes;
-    if (b >= kLanes) M_ST(drain(b - kLanes));
-    for (int64_t t = 0; t < pb.tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[pb.tok0 + t];
+  const int nf = (int)groups.size();
+  for (int f = 0; f < nf; ++f) {
+    const Group& g = groups[(size_t)f];
+    const Batch& p0 = plan[(size_t)g.b0];
+    const Batch& pl = plan[(size_t)(g.b0 + g.nb - 1)];
+    const int count = pl.first + pl.count - p0.first;
+    const int64_t tokens = pl.tok0 + pl.tokens - p0.tok0;
+    const int k = f % kLanes;
+    if (f >= kLanes) M_ST(drain(f - kLanes));
+    for (int64_t t = 0; t < tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[p0.tok0 + t];
     Lane& L = m->lane[k];
-    M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)pb.tokens * 4, hipMemcpyHostToDevice,
+    M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)tokens * 4, hipMemcpyHostToDevice,
                            L.stream));
-    M_ST(prepare(m, L, lengths + pb.first, pb.count));
-    M_ST(run(m, L, P.ids_dev[k], pb.count, P.out_dev[k], P.flags_dev[k]));
+    M_ST(prepare(m, L, lengths + p0.first, count));
+    M_ST(run(m, L, P.ids_dev[k], count, P.out_dev[k], P.flags_dev[k]));
+    if (g.nb > 1) {
+      M_CHECK(launch_row_nonfinite(P.out_dev[k], count, (int)H, P.rows_dev[k], L.stream));
+      M_CHECK(hipMemcpyAsync(P.rows_pin[k], P.rows_dev[k], (size_t)count * 4,
+                             hipMemcpyDeviceToHost, L.stream));
+    }
     const void* dev_out = P.out_dev[k];
     if (out_dtype == FL_F16) {
-      M_CHECK(launch_cast(P.out_dev[k], FL_F32, P.out16_dev[k], FL_F16, (int64_t)pb.count * H, 0,
+      M_CHECK(launch_cast(P.out_dev[k], FL_F32, P.out16_dev[k], FL_F16, (int64_t)count * H, 0,
                           L.stream));
       dev_out = P.out16_dev[k];
     }
-    M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)pb.count * H * osz, hipMemcpyDeviceToHost,
+    M_CHECK(hipMemcpyAsync(P.out_pin[k], dev_out, (size_t)count * H * osz, hipMemcpyDeviceToHost,
                            L.stream));
     M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, L.stream));
     M_CHECK(hipEventRecord(P.d2h[k], L.stream));
   }
-  for (int b = std::max(0, nb - kLanes); b < nb; ++b) M_ST(drain(b));
+  for (int f = std::max(0, nf - kLanes); f < nf; ++f) M_ST(drain(f));
   // fl_model_status then reports the last batch (drained, so its forward is done).
-  M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[(nb - 1) % kLanes], 8, hipMemcpyDeviceToDevice, cs));
-  if (nbatches) *nbatches = nb;
+  const Group& gl = groups.back();
+  const int kl = (nf - 1) % kLanes;
+  if (gl.nb == 1) {
+    M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[kl], 8, hipMemcpyDeviceToDevice, cs));
+  } else {
+    const int st[2] = {batch_flag(gl, gl.b0 + gl.nb - 1, kl), P.flags_pin[kl][1]};
+    M_CHECK(hipMemcpyAsync(L0.flags, st, 8, hipMemcpyHostToDevice, cs));
+    M_CHECK(hipStreamSynchronize(cs));
+  }
+  if (nbatches) *nbatches = (int)plan.size();
   return FL_OK;
 }
 

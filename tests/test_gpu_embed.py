@@ -11,7 +11,8 @@ overlapped on their own streams.
   composition only moves rows).
 * A sample is checked against the CPU oracle at the fp16 bar.
 * The per-batch NaN flag (embeddings.go:757-764) marks exactly the sequences
-  of the batch whose output holds a NaN.
+  of the batch whose output holds a NaN, also where several batches of the
+  plan run as one forward, and fl_model_status reports the plan's last batch.
 """
 import sys
 import time
@@ -142,5 +143,36 @@ def test_embed_nan_flag_per_batch(fl, ctx):
         assert nb == 3
         assert nan.tolist() == [False] * 4 + [True] * 4 + [False] * 4
         assert np.isnan(out[5]).any() and np.isfinite(out[:4]).all() and np.isfinite(out[8:]).all()
+        assert m.status() == (False, False)   # the plan's last batch is clean
+        # NaN in the last batch (sequence 10); then the whole call as one batch.
+        ids2 = synth.make_ids(lengths, seed=3)
+        ids2[10 * 40 + 3] = 777
+        _o, nan2, _nb = m.embed(ids2, lengths, max_seqs=4, max_tokens=16384)
+        assert nan2.tolist() == [False] * 8 + [True] * 4
+        assert m.status() == (True, False)
+        _o, nan3, nb3 = m.embed(ids, lengths, max_seqs=12, max_tokens=16384)
+        assert nb3 == 1 and nan3.all() and m.status() == (True, False)
+        m.forward(ids[:40], lengths[:1])
+        assert m.status() == (False, False)
+        # Several forwards on the lanes (well over 65536 tokens): the flags
+        # follow the plan's batches, the vectors equal one forward per batch.
+        lengths = synth.ragged_lengths(1500, seed=41, median=128.0)
+        ids = synth.make_ids(lengths, seed=42)
+        starts = np.concatenate([[0], np.cumsum(lengths)])
+        bad_seq = 1111
+        ids[starts[bad_seq] + 1] = 777
+        plan = reference_plan(lengths, 512, 16384)
+        log(f"embed with NaN: T={lengths.sum()} batches={len(plan)}")
+        out, nan, nb = m.embed(ids, lengths, max_seqs=512, max_tokens=16384)
+        assert nb == len(plan) and lengths.sum() > 3 * 65536
+        want_nan = np.zeros(len(lengths), bool)
+        for first, count in plan:
+            if first <= bad_seq < first + count:
+                want_nan[first:first + count] = True
+        assert (nan == want_nan).all()
+        assert np.isnan(out[bad_seq]).any() and np.isfinite(out[~want_nan]).all()
+        for first, count in plan[:2] + plan[-2:]:
+            want = m.forward(ids[starts[first]:starts[first + count]], lengths[first:first + count])
+            np.testing.assert_array_equal(out[first:first + count], want)
     finally:
         m.close()
