@@ -373,8 +373,11 @@ class Context:
 
 
 def plan_batches(lengths, max_seqs: int = 512, max_tokens: int = 16384):
-    """The (first sequence, count) batches fl_model_embed runs: the batching
-    loop of runInferenceOnDevice (embeddings.go:704-731)."""
+    """The (first sequence, count) batches of fl_model_embed's plan: the
+    batching loop of runInferenceOnDevice (embeddings.go:704-731).  The
+    library computes consecutive batches of the plan together, in forwards
+    of up to 65536 tokens; the vectors and per-batch NaN flags are those of
+    one forward per batch."""
     plan, i, n = [], 0, len(lengths)
     while i < n:
         size, tokens = 0, 0
