@@ -503,6 +503,21 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_lds_kernel(GemmParams p) {
 // each lane produces 16 contiguous bytes at a time.  The bias is read in
 // packed order.
 // ---------------------------------------------------------------------------
+// One 16x16x32 MFMA with 16-bit operands given as raw 16-byte fragments.
+template <typename T> struct MfmaFrag;
+template <> struct MfmaFrag<_Float16> {
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                               __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct MfmaFrag<__bf16> {
+  __device__ static inline void mma(float4_t& c, const u32x4_t& a, const u32x4_t& b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+
 template <typename T>
 __device__ inline u32x4_t pack8(float4_t a, float4_t b) {
   if constexpr (Elem<T>::dtype == F16) {
@@ -1106,6 +1121,106 @@ static int persistent_grid(int ntiles) {
   return grid;
 }
 
+// ---------------------------------------------------------------------------
+// Few-row form of the four-wave GEMM.  With a single 256-row block the
+// four-wave kernel runs N / 256 tiles, each walking the whole K on one CU
+// (FFN-down at 16 tokens: 3 workgroups, 96 K steps).  Here a workgroup owns
+// one epilogue unit, 16 rows x 64 packed features: wave w multiplies feature
+// block w (16 features) over the whole K with the same 16x16x32 MFMA, the
+// same operand roles (weights as the first operand) and the same K order
+// starting from zero, so every accumulator holds the bits the four-wave
+// kernel's does; the unit then goes through the same epilogue math
+// (w4_epilogue_block).  Outputs are therefore identical, and a sequence's
+// vector still does not depend on the batch around it.  Fragments come
+// straight from global memory (weights tiled, activations tiled or
+// row-major), PF K steps ahead in registers.  Rows past M are computed from
+// rows M-1 (row-major A) or the padding rows (tiled A) and not stored.
+// ---------------------------------------------------------------------------
+template <typename T, int EPI, int MATH, bool HB>
+__global__ void __launch_bounds__(256) gemm_small_kernel(GemmParams p) {
+  constexpr int PF = 16;  // K steps in flight per wave
+  __shared__ float4_t accs[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nbase = blockIdx.x * 64;      // the unit's first packed feature
+  const int m0 = blockIdx.y * 16;         // the unit's first row
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nk = p.K / 32;
+  const T* W = (const T*)p.B;
+  const T* A = (const T*)p.A;
+  const int n = nbase + wave * 16 + fr;   // this lane's packed feature (weight row)
+  const int m = m0 + fr;                  // this lane's row
+  const int ma = p.epi.a_tiled ? m : min(m, p.M - 1);
+  // Packed row n of the tiled weights: the tiled activation layout over K.
+  auto wptr = [&](int s) __attribute__((always_inline)) {
+    return (const u32x4_t*)(W + tiled_act_offset(n, s * 32 + fg * 8, p.K));
+  };
+  auto aptr = [&](int s) __attribute__((always_inline)) {
+    const int k = s * 32 + fg * 8;
+    return (const u32x4_t*)(A + (p.epi.a_tiled ? tiled_act_offset(ma, k, p.K)
+                                               : (size_t)ma * p.lda + k));
+  };
+  u32x4_t wf[PF], af[PF];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const int s = min(j, nk - 1);
+    wf[j] = *wptr(s);
+    af[j] = *aptr(s);
+  }
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  int s0 = 0;
+  for (; s0 + PF <= nk; s0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      MfmaFrag<T>::mma(acc, wf[j], af[j]);
+      // The step PF ahead (clamped: loads past the end repeat the last step
+      // and are never used), issued without a branch so the waits stay exact.
+      const int s = min(s0 + PF + j, nk - 1);
+      wf[j] = *wptr(s);
+      af[j] = *aptr(s);
+    }
+  }
+  // The last nk % PF steps (a multiple of 4: K % 128 == 0) sit in slots
+  // 0 .. nk % PF - 1.
+#pragma unroll
+  for (int q = 0; q < PF / 4 - 1; ++q) {
+    if (s0 + 4 * q + 4 > nk) break;
+#pragma unroll
+    for (int j = 4 * q; j < 4 * q + 4; ++j) MfmaFrag<T>::mma(acc, wf[j], af[j]);
+  }
+  accs[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float4_t v[4] = {accs[0][lane], accs[1][lane], accs[2][lane], accs[3][lane]};
+  const int r = lane & 15, g = lane >> 4;
+  const int row = m0 + r;
+  float4_t bv[4];
+  if constexpr (HB) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) bv[f] = *(const float4_t*)(p.epi.bias + nbase + f * 16 + g * 4);
+  }
+  float4_t cs[4];
+  if constexpr (EPI == EPI_ROPE) {
+    const float2* table = nbase < p.epi.q_cols ? p.epi.rope_cs_q : p.epi.rope_cs;
+    const int pos = p.epi.pos[min(row, p.M - 1)];
+    const float4_t* src = (const float4_t*)(table + (size_t)pos * 32 + g * 8);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cs[k] = src[k];
+  }
+  auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
+    if (row >= p.M) return;
+    T* dst = (T*)p.C + (EPI == EPI_SWIGLU && p.epi.out_tiled ? tiled_act_offset(row, col, p.ldc)
+                                                             : (size_t)row * p.ldc + col);
+    *(u32x4_t*)dst = pack8<T>(a, b);
+  };
+  auto bias_at = [&](int f) { return bv[f]; };
+  auto rope_at = [&](int k) { return cs[k]; };
+  if (EPI == EPI_ROPE && nbase >= p.epi.rope_cols)
+    w4_epilogue_block<T, EPI, MATH, HB, false>(p, v, nbase, lane, bias_at, rope_at, put);
+  else
+    w4_epilogue_block<T, EPI, MATH, HB, true>(p, v, nbase, lane, bias_at, rope_at, put);
+}
+
 // The four-wave kernel's K loop runs in groups of four steps with at least
 // two groups per tile; its RoPE epilogue gives both 64-feature heads of a
 // wave the same table and rotation.
@@ -1122,6 +1237,21 @@ static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
   const int grid = persistent_grid(ntiles);
   hipLaunchKernelGGL((gemm_w4_kernel<T, EPI, MATH, 4>), dim3(grid), dim3(256), 0, s,
                      p, ntiles);
+  return hipGetLastError();
+}
+
+// The few-row kernel takes a four-wave GEMM of at most kSmallRows rows:
+// there the four-wave kernel has one 256-row block, so at most N / 256
+// workgroups walking the whole K each.
+constexpr int kSmallRows = 256;
+
+template <typename T, int EPI, int MATH>
+static hipError_t launch_small(const GemmParams& p, hipStream_t s) {
+  const dim3 grid(p.N / 64, (p.M + 15) / 16);
+  if (EPI != EPI_ROPE && p.epi.bias)
+    hipLaunchKernelGGL((gemm_small_kernel<T, EPI, MATH, true>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_small_kernel<T, EPI, MATH, false>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -1145,7 +1275,10 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     // layout (gemm_nt_supported).
     if (p.epi.layout >= PACK_LANE16) {
       if constexpr (w4_epilogue_ok(EPI, MATH)) {
-        if (gemm_w4_ok(p)) return launch_w4<T, EPI, MATH>(p, s);
+        if (gemm_w4_ok(p)) {
+          if (p.M <= kSmallRows) return launch_small<T, EPI, MATH>(p, s);
+          return launch_w4<T, EPI, MATH>(p, s);
+        }
       }
       return hipErrorInvalidValue;
     }
