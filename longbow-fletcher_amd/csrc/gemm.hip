@@ -1240,10 +1240,24 @@ static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The few-row kernel takes a four-wave GEMM of at most kSmallRows rows:
-// there the four-wave kernel has one 256-row block, so at most N / 256
-// workgroups walking the whole K each.
-constexpr int kSmallRows = 256;
+// Whether the few-row kernel beats the four-wave kernel on this GEMM, from
+// per-launch times measured on single-sequence forwards of 128-1024 tokens
+// (Nomic and BERT-base projections): the four-wave kernel takes ~0.55 us per
+// K step and ~10 us more per round of tiles, whatever the rows; the few-row
+// kernel ~9 us plus 0.25 ns per (unit, K step) with tiled activations, twice
+// that with row-major ones (16 rows x 16 bytes at the row pitch per load).
+// At 512 tokens that sends FFN-down (96 K steps, 3 column tiles) and O to the
+// few-row kernel and keeps FFN-up (96 units per 16 rows) on the four-wave one.
+static bool gemm_small_better(const GemmParams& p) {
+  if (p.M > 4096) return false;
+  const double nk = p.K / 32;
+  const double units = (double)((p.M + 15) / 16) * (p.N / 64);
+  const double small_us = units * nk * (p.epi.a_tiled ? 0.25e-3 : 0.5e-3) + 9.0;
+  const int cus = cu_count();
+  const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
+  const double w4_us = ((ntiles + cus - 1) / cus) * (0.55 * nk + 10.0);
+  return small_us < w4_us;
+}
 
 template <typename T, int EPI, int MATH>
 static hipError_t launch_small(const GemmParams& p, hipStream_t s) {
@@ -1276,7 +1290,7 @@ static hipError_t launch_pick(const GemmParams& p, hipStream_t s) {
     if (p.epi.layout >= PACK_LANE16) {
       if constexpr (w4_epilogue_ok(EPI, MATH)) {
         if (gemm_w4_ok(p)) {
-          if (p.M <= kSmallRows) return launch_small<T, EPI, MATH>(p, s);
+          if (gemm_small_better(p)) return launch_small<T, EPI, MATH>(p, s);
           return launch_w4<T, EPI, MATH>(p, s);
         }
       }
