@@ -354,6 +354,19 @@ def main():
         for _ in range(reps):
             model.embed(ids, lengths, len(lengths), big)
         e2e["whole_batch_embeddings_per_s"] = round(len(lengths) * reps / (time.perf_counter() - t0), 1)
+        # Latency of a short request (one sequence, host ids in, host vector
+        # out): the few-row GEMM path.
+        short = {}
+        for n_tok in (16, 128):
+            sl = np.array([min(n_tok, int(lengths[0]))], np.int64)
+            sid = ids[:int(sl[0])]
+            for _ in range(3):
+                model.forward(sid, sl)
+            t0 = time.perf_counter()
+            for _ in range(20):
+                model.forward(sid, sl)
+            short[f"ms_per_call_{int(sl[0])}_tokens"] = round((time.perf_counter() - t0) / 20 * 1e3, 3)
+        e2e["short_request"] = short
         log(f"end to end: {e2e}")
 
     per_op = None
