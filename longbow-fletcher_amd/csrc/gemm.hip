@@ -1244,15 +1244,15 @@ static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
 // per-launch times measured on single-sequence forwards of 128-1024 tokens
 // (Nomic and BERT-base projections): the four-wave kernel takes ~0.55 us per
 // K step and ~10 us more per round of tiles, whatever the rows; the few-row
-// kernel ~9 us plus 0.25 ns per (unit, K step) with tiled activations, twice
-// that with row-major ones (16 rows x 16 bytes at the row pitch per load).
+// kernel ~9 us plus 0.25 ns per (unit, K step) with tiled activations,
+// 0.6 ns with row-major ones (16 rows x 16 bytes at the row pitch per load).
 // At 512 tokens that sends FFN-down (96 K steps, 3 column tiles) and O to the
 // few-row kernel and keeps FFN-up (96 units per 16 rows) on the four-wave one.
 static bool gemm_small_better(const GemmParams& p) {
   if (p.M > 4096) return false;
   const double nk = p.K / 32;
   const double units = (double)((p.M + 15) / 16) * (p.N / 64);
-  const double small_us = units * nk * (p.epi.a_tiled ? 0.25e-3 : 0.5e-3) + 9.0;
+  const double small_us = units * nk * (p.epi.a_tiled ? 0.25e-3 : 0.6e-3) + 9.0;
   const int cus = cu_count();
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
   const double w4_us = ((ntiles + cus - 1) / cus) * (0.55 * nk + 10.0);
