@@ -29,11 +29,12 @@ def log(msg):
     print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
 
 
-@pytest.mark.parametrize("family", ["nomic", "bert_base", "minilm"])
-def test_alone_equals_in_batch(fl, ctx, family):
+@pytest.mark.parametrize("family,dtype", [("nomic", "f16"), ("bert_base", "f16"),
+                                          ("minilm", "f16"), ("nomic", "bf16")])
+def test_alone_equals_in_batch(fl, ctx, family, dtype):
     cfg = getattr(synth, family)(layers=2)
     w = synth.make_weights(cfg)
-    m = fl.Model(ctx, cfg, dtype=fl.F16)
+    m = fl.Model(ctx, cfg, dtype=fl.F16 if dtype == "f16" else fl.BF16)
     try:
         m.load(w)
         lengths = np.array(LENGTHS + FILL, np.int64)
