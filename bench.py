@@ -372,20 +372,24 @@ def main():
     per_op = None
     if not a.no_per_op:
         # The per-op path: bert.go's ForwardBatch op by op through the C ABI,
-        # the path the unchanged Go model takes (perop.py), same batch.
+        # the path the unchanged Go model takes (perop.py: the Tensor calls of
+        # bert.go on the binding's backend, fp32 master stream included),
+        # same batch.
         from importlib import import_module
         perop = import_module(fl.__name__ + ".perop")
-        pm = perop.PerOpModel(ctx, cfg, weights, w.dtype,
-                              fl.MATH_REFERENCE if w.dtype == fl.F32 else fl.MATH_EXACT)
-        pm.forward_device(ids, lengths).free()
-        ctx.synchronize()
+        dev = import_module(fl.__name__ + ".device")
+        be = dev.RocmBackend(0, w.dtype, rope_base=cfg.rope_base)
+        pm = perop.PerOpModel(be, cfg, weights)
+        be.PutTensor(pm.forward_device(ids, lengths))
+        be.Synchronize()
         reps = 3
         t0 = time.perf_counter()
         for _ in range(reps):
-            pm.forward_device(ids, lengths).free()
-        ctx.synchronize()
+            be.PutTensor(pm.forward_device(ids, lengths))
+        be.Synchronize()
         dt = (time.perf_counter() - t0) / reps
         pm.close()
+        be.close()
         per_op = {"embeddings_per_s": round(len(lengths) / dt, 1), "ms_per_step": round(dt * 1e3, 3),
                   "steps": reps}
         log(f"per-op path: {per_op}")

@@ -16,7 +16,26 @@
  *    working.)
  *  - Buffers are plain device pointers obtained from fl_alloc; views are
  *    pointer arithmetic on them.  Tensors are 2-D row-major; `ld` arguments are
- *    row strides in elements.
+ *    row strides in elements.  Tensor.Slice of whole rows (all columns) is
+ *    such a view, not a copy, as in the reference's Metal backend
+ *    (metal_darwin.go:487-521): src + r0 * cols * element size, owned by the
+ *    tensor it points into (never passed to fl_free); writes through it land
+ *    in that tensor.  Every entry point accepts views.  Other slices are
+ *    copies (fl_slice).
+ *  - Every per-op entry point checks each operand's byte extent against the
+ *    fl_alloc buffer the pointer lies in (views included) and returns
+ *    FL_ERR_INVALID, before anything is enqueued, for an operand that would
+ *    run past the end of its buffer (e.g. an fp16 buffer passed as fp32).
+ *    Pointers from other allocators are not sized and not checked.
+ *  - Operands of different storage types follow the reference's Metal
+ *    backend: Linear's result and arithmetic take the weight's type, its input
+ *    is converted (metal_darwin.go:806-829); Add / AddLayerNorm convert the
+ *    other operand to the receiver's type (:603-619, 798-804).  Conversions
+ *    happen in the kernels (loads, or the producing kernel's store), not in
+ *    extra passes over the data, except the first time an fp32 tensor is
+ *    read by a 16-bit Linear (one conversion, kept for the Q, K and V
+ *    projections of the same hidden state and refreshed by the LayerNorm
+ *    that next rewrites it).
  *  - All work of a context is enqueued in order on the context's HIP stream;
  *    entry points that hand data back to the host synchronise that stream,
  *    and the others return without waiting for the device.
@@ -157,14 +176,19 @@ int fl_download_f32(fl_context *ctx, float *dst, const void *src, int dtype, int
 int fl_gemm(fl_context *ctx, int dtype, int trans_a, int trans_b, int m, int n, int k,
             float alpha, const void *a, int lda, const void *b, int ldb, void *c, int ldc);
 /* Tensor.Linear / LinearActivation (device.go:75-81; cpu_backend.go:612-660):
- * out = act(x * W + bias).  x is [rows x in_cols]; W is [in_cols x out_cols]
- * (FL_W_IN_OUT) or [out_cols x in_cols] (FL_W_OUT_IN); bias is dtype-typed
- * [out_cols] or NULL.  For FL_ACT_SWIGLU out has out_cols/2 columns:
- * silu(first half) * second half (cpu_backend.go:636-654). */
-int fl_linear(fl_context *ctx, int dtype, const void *x, int rows, int in_cols, const void *w,
-              int w_layout, int out_cols, const void *bias, int act, int math, void *out);
-/* Tensor.Add (device.go:45): t += other, n elements. */
-int fl_add(fl_context *ctx, int dtype, void *t, const void *other, int64_t n);
+ * out = act(x * W + bias).  x is [rows x in_cols] of x_dtype; W is
+ * [in_cols x out_cols] (FL_W_IN_OUT) or [out_cols x in_cols] (FL_W_OUT_IN)
+ * of w_dtype; bias is w_dtype [out_cols] or NULL; out is w_dtype (the
+ * result follows the weight, metal_darwin.go:818-829: bert.go:253-258 keeps
+ * an fp32 hidden state that fp16 weights read, bert.go:614-616).  For
+ * FL_ACT_SWIGLU out has out_cols/2 columns: silu(first half) * second half
+ * (cpu_backend.go:636-654). */
+int fl_linear(fl_context *ctx, int x_dtype, const void *x, int rows, int in_cols, int w_dtype,
+              const void *w, int w_layout, int out_cols, const void *bias, int act, int math,
+              void *out);
+/* Tensor.Add (device.go:45): t += other, n elements; other (other_dtype) is
+ * converted to t's dtype (metal_darwin.go:603-619). */
+int fl_add(fl_context *ctx, int dtype, void *t, int other_dtype, const void *other, int64_t n);
 /* Tensor.AddScalar (device.go:48). */
 int fl_add_scalar(fl_context *ctx, int dtype, void *t, int64_t n, float v);
 /* Tensor.Scale (device.go:51). */
@@ -178,9 +202,11 @@ int fl_activation(fl_context *ctx, int dtype, void *t, int rows, int cols, int a
  * (bert.go:278-280 keeps LayerNorm parameters in fp32). */
 int fl_layernorm(fl_context *ctx, int dtype, void *t, int rows, int cols, const float *gamma,
                  const float *beta, float eps);
-/* Tensor.AddLayerNorm (device.go:64-72): t = LayerNorm(t + residual). */
-int fl_add_layernorm(fl_context *ctx, int dtype, void *t, const void *residual, int rows,
-                     int cols, const float *gamma, const float *beta, float eps);
+/* Tensor.AddLayerNorm (device.go:64-72): t = LayerNorm(t + residual), the
+ * residual (res_dtype) converted to t's dtype on load: bert.go:813-824 adds
+ * an fp16 branch to the fp32 hidden state. */
+int fl_add_layernorm(fl_context *ctx, int dtype, void *t, int res_dtype, const void *residual,
+                     int rows, int cols, const float *gamma, const float *beta, float eps);
 /* Tensor.Gather (device.go:72): out[i] = table[idx[i]]; idx on the host. */
 int fl_gather_rows(fl_context *ctx, int dtype, const void *table, int rows, int cols,
                    const int64_t *idx, int n, void *out);
@@ -208,8 +234,10 @@ int fl_cast(fl_context *ctx, const void *src, int src_dtype, void *dst, int dst_
 /* Tensor.HasNaN (device.go:111-112; cpu_backend.go:845-863): *out = 1 if any
  * element is NaN or +-Inf (synchronises). */
 int fl_has_nan(fl_context *ctx, const void *t, int dtype, int64_t n, int *out);
-/* Tensor.Slice (device.go:34): copy rows [r0, r1) x cols [c0, c1) of a
- * [rows x cols] tensor into a dense [(r1-r0) x (c1-c0)] buffer. */
+/* Tensor.Slice (device.go:34) of a column range: copy rows [r0, r1) x cols
+ * [c0, c1) of a [rows x cols] tensor into a dense [(r1-r0) x (c1-c0)] buffer
+ * (metal_darwin.go:522-541).  A slice of all columns is a view (see the
+ * conventions above), not a call. */
 int fl_slice(fl_context *ctx, int dtype, const void *src, int rows, int cols, int r0, int r1,
              int c0, int c1, void *dst);
 /* Masked mean-pool (+ L2 normalise when l2 != 0) over packed sequences:

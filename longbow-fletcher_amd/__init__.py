@@ -82,14 +82,14 @@ _SIGS = {
     "fl_upload_f32": ([_vp, _vp, _i, _vp, _i64, _i], _i),
     "fl_download_f32": ([_vp, _vp, _vp, _i, _i64], _i),
     "fl_gemm": ([_vp, _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _i], _i),
-    "fl_linear": ([_vp, _i, _vp, _i, _i, _vp, _i, _i, _vp, _i, _i, _vp], _i),
-    "fl_add": ([_vp, _i, _vp, _vp, _i64], _i),
+    "fl_linear": ([_vp, _i, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _vp], _i),
+    "fl_add": ([_vp, _i, _vp, _i, _vp, _i64], _i),
     "fl_add_scalar": ([_vp, _i, _vp, _i64, _f], _i),
     "fl_scale": ([_vp, _i, _vp, _i64, _f], _i),
     "fl_add_bias": ([_vp, _i, _vp, _i, _i, _vp], _i),
     "fl_activation": ([_vp, _i, _vp, _i, _i, _i, _i], _i),
     "fl_layernorm": ([_vp, _i, _vp, _i, _i, _vp, _vp, _f], _i),
-    "fl_add_layernorm": ([_vp, _i, _vp, _vp, _i, _i, _vp, _vp, _f], _i),
+    "fl_add_layernorm": ([_vp, _i, _vp, _i, _vp, _i, _i, _vp, _vp, _f], _i),
     "fl_gather_rows": ([_vp, _i, _vp, _i, _i, _vp, _i, _vp], _i),
     "fl_rope": ([_vp, _i, _vp, _i, _i, _i, _i, _f], _i),
     "fl_rope_varlen": ([_vp, _i, _vp, _vp, _i, _i, _i, _f], _i),
@@ -189,6 +189,15 @@ class DeviceArray:
         check(lib().fl_copy_to_host(self.ctx.h, out.ctypes.data, self.ptr, self.nbytes))
         return out.reshape(self.shape)
 
+    def rows_view(self, r0: int, r1: int) -> "DeviceArray":
+        """Rows [r0, r1) of a 2-D tensor as a non-owning view (Tensor.Slice of
+        all columns, metal_darwin.go:487-521): writes through it land here."""
+        rows, cols = self.shape
+        if not 0 <= r0 < r1 <= rows:
+            raise FletcherError(ERR_INVALID, "Slice: invalid dimensions")
+        return DeviceArray(self.ctx, self.ptr + r0 * cols * _ESZ[self.dtype], (r1 - r0, cols),
+                           self.dtype, owned=False)
+
     def free(self):
         if self.owned and self.ptr:
             check(lib().fl_free(self.ctx.h, self.ptr))
@@ -283,15 +292,18 @@ class Context:
 
     def linear(self, x: DeviceArray, w: DeviceArray, bias=None, act=ACT_IDENTITY,
                math=MATH_REFERENCE, w_layout=W_IN_OUT):
+        """out = act(x W + bias); the result has W's storage type and x is
+        converted to it (Linear on the reference's Metal backend)."""
         rows, k = x.shape
         n = w.shape[1] if w_layout == W_IN_OUT else w.shape[0]
-        out = self.result((rows, n // 2 if act == ACT_SWIGLU else n), x.dtype)
-        check(lib().fl_linear(self.h, x.dtype, x.ptr, rows, k, w.ptr, w_layout, n, _ptr(bias),
-                              act, math, out.ptr))
+        out = self.result((rows, n // 2 if act == ACT_SWIGLU else n), w.dtype)
+        check(lib().fl_linear(self.h, x.dtype, x.ptr, rows, k, w.dtype, w.ptr, w_layout, n,
+                              _ptr(bias), act, math, out.ptr))
         return out
 
     def add(self, t: DeviceArray, o: DeviceArray):
-        check(lib().fl_add(self.h, t.dtype, t.ptr, o.ptr, t.size))
+        """t += o (o converted to t's storage type)."""
+        check(lib().fl_add(self.h, t.dtype, t.ptr, o.dtype, o.ptr, t.size))
 
     def add_scalar(self, t: DeviceArray, v: float):
         check(lib().fl_add_scalar(self.h, t.dtype, t.ptr, t.size, v))
@@ -310,8 +322,9 @@ class Context:
                                  beta.ptr, eps))
 
     def add_layernorm(self, t, residual, gamma, beta, eps):
-        check(lib().fl_add_layernorm(self.h, t.dtype, t.ptr, residual.ptr, t.shape[0],
-                                     t.shape[1], gamma.ptr, beta.ptr, eps))
+        """t = LayerNorm(t + residual), the residual converted to t's type."""
+        check(lib().fl_add_layernorm(self.h, t.dtype, t.ptr, residual.dtype, residual.ptr,
+                                     t.shape[0], t.shape[1], gamma.ptr, beta.ptr, eps))
 
     def gather(self, table: DeviceArray, idx) -> DeviceArray:
         idx = np.ascontiguousarray(idx, np.int64)

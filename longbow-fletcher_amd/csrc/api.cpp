@@ -39,7 +39,7 @@ int activate(fl_context* ctx) {
 
 int device_alloc(fl_context* ctx, size_t bytes, void** out) {
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+  hipError_t e = malloc_retry(ctx, &p, bytes ? bytes : 16);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
   ctx->allocated += (int64_t)bytes;
   *out = p;
@@ -69,7 +69,7 @@ void* workspace(fl_context* ctx, size_t bytes, int* status) {
   size_t sz = 1 << 20;
   while (sz < bytes) sz <<= 1;
   void* p = nullptr;
-  e = hipMalloc(&p, sz);
+  e = malloc_retry(ctx, &p, sz);
   if (e != hipSuccess) {
     *status = hip_fail(e, "hipMalloc(workspace)");
     return nullptr;
@@ -110,7 +110,7 @@ const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int
   t.cs = nullptr;
   t.cap = 0;
   void* p = nullptr;
-  e = hipMalloc(&p, host.size() * sizeof(float2));
+  e = malloc_retry(ctx, &p, host.size() * sizeof(float2));
   if (e != hipSuccess) {
     *status = hip_fail(e, "hipMalloc(rope)");
     return nullptr;
@@ -147,8 +147,23 @@ using namespace fl;
 
 static bool valid_dtype(int dt) { return dt == FL_F32 || dt == FL_F16 || dt == FL_BF16; }
 
-// What a PackKey's `kind` packs.
-enum PackKind { PK_GEMM_B = 1, PK_LINEAR_W = 2, PK_LINEAR_BIAS = 3 };
+// Bytes spanned by a [rows x cols] operand with row stride ld.
+static int64_t span(int64_t rows, int64_t cols, int64_t ld, int dtype) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return ((rows - 1) * ld + cols) * (int64_t)dtype_size(dtype);
+}
+
+// Rejects an operand that runs past the end of its fl_alloc buffer before
+// anything is enqueued.
+#define FL_EXTENT(ptr, bytes, what)                                         \
+  do {                                                                      \
+    int _fl_x = check_extent(ctx, (ptr), (int64_t)(bytes), (what));        \
+    if (_fl_x) return _fl_x;                                                \
+  } while (0)
+
+// What a PackKey's `kind` packs.  PK_CONVERTED: a copy of an activation in
+// another storage type (key.dtype), for a Linear whose weight has that type.
+enum PackKind { PK_GEMM_B = 1, PK_LINEAR_W = 2, PK_LINEAR_BIAS = 3, PK_CONVERTED = 4 };
 
 // The packed form of a weight: kept between calls when the source is an
 // fl_alloc buffer (repacked after it is written), else packed into `fallback`
@@ -314,7 +329,8 @@ static int alloc_block(fl_context* ctx, int64_t bytes, bool zero, void** out) {
       return hip_fail(e, "hipMemsetAsync");
     }
   }
-  ctx->live[(uintptr_t)p] = fl_context::Live{cls, ctx->device, ++ctx->gen_counter};
+  ctx->live[(uintptr_t)p] =
+      fl_context::Live{cls, bytes > 0 ? (size_t)bytes : 0, ctx->device, ++ctx->gen_counter};
   *out = p;
   return FL_OK;
 }
@@ -374,6 +390,7 @@ int fl_copy_to_device(fl_context* ctx, void* dst, const void* src, int64_t bytes
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
   if (bytes == 0) return FL_OK;
+  FL_EXTENT(dst, bytes, "fl_copy_to_device dst");
   note_write(ctx, dst);
   // The host buffer may be reused on return: small copies go through a
   // pinned slot without waiting, large ones wait.
@@ -384,6 +401,7 @@ int fl_copy_to_host(fl_context* ctx, void* dst, const void* src, int64_t bytes) 
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
   if (bytes == 0) return FL_OK;
+  FL_EXTENT(src, bytes, "fl_copy_to_host src");
   FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx->stream));
   FL_CHECK_LAUNCH(hipStreamSynchronize(ctx->stream));
   return FL_OK;
@@ -393,6 +411,8 @@ int fl_copy_device(fl_context* ctx, void* dst, const void* src, int64_t bytes) {
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && (!dst || !src))) return fail(FL_ERR_INVALID, "bad copy");
   if (bytes == 0) return FL_OK;
+  FL_EXTENT(dst, bytes, "fl_copy_device dst");
+  FL_EXTENT(src, bytes, "fl_copy_device src");
   note_write(ctx, dst);
   FL_CHECK_LAUNCH(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, ctx->stream));
   return FL_OK;
@@ -402,6 +422,7 @@ int fl_memset(fl_context* ctx, void* ptr, int value, int64_t bytes) {
   FL_ENTER(ctx);
   if (bytes < 0 || (bytes > 0 && !ptr)) return fail(FL_ERR_INVALID, "bad memset");
   if (bytes == 0) return FL_OK;
+  FL_EXTENT(ptr, bytes, "fl_memset");
   note_write(ctx, ptr);
   FL_CHECK_LAUNCH(hipMemsetAsync(ptr, value, (size_t)bytes, ctx->stream));
   return FL_OK;
@@ -413,6 +434,7 @@ int fl_upload_f32(fl_context* ctx, void* dst, int dtype, const float* src, int64
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!dst || !src)))
     return fail(FL_ERR_INVALID, "bad upload");
   if (n == 0) return FL_OK;
+  FL_EXTENT(dst, n * (int64_t)dtype_size(dtype), "fl_upload_f32 dst");
   note_write(ctx, dst);
   if (dtype == FL_F32) return stage_upload(ctx, dst, src, (size_t)n * 4);
   if (rounding == FL_ROUND_TRUNCATE && dtype != FL_F16)
@@ -431,6 +453,7 @@ int fl_download_f32(fl_context* ctx, float* dst, const void* src, int dtype, int
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!dst || !src)))
     return fail(FL_ERR_INVALID, "bad download");
   if (n == 0) return FL_OK;
+  FL_EXTENT(src, n * (int64_t)dtype_size(dtype), "fl_download_f32 src");
   const void* from = src;
   if (dtype != FL_F32) {
     int st;
@@ -454,6 +477,14 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
   if (!valid_dtype(dtype) || m < 0 || n < 0 || k < 0 || !a || !b || !c)
     return fail(FL_ERR_INVALID, "fl_gemm: bad arguments");
   if (m == 0 || n == 0) return FL_OK;
+  // A is [m x k] ([k x m] when trans_a), B [k x n] ([n x k] when trans_b).
+  const int ar = trans_a ? k : m, ac = trans_a ? m : k;
+  const int br = trans_b ? n : k, bc = trans_b ? k : n;
+  if (lda < std::max(ac, 1) || ldb < std::max(bc, 1) || ldc < n)
+    return fail(FL_ERR_INVALID, "fl_gemm: leading dimension smaller than the row");
+  FL_EXTENT(a, span(ar, ac, lda, dtype), "fl_gemm A");
+  FL_EXTENT(b, span(br, bc, ldb, dtype), "fl_gemm B");
+  FL_EXTENT(c, span(m, n, ldc, dtype), "fl_gemm C");
   note_write(ctx, c);
   GemmEpilogue epi;
   if (!trans_a && alpha == 1.0f) {
@@ -506,34 +537,58 @@ int fl_gemm(fl_context* ctx, int dtype, int trans_a, int trans_b, int m, int n, 
   return FL_OK;
 }
 
-int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, const void* w,
-              int w_layout, int out_cols, const void* bias, int act, int math, void* out) {
+int fl_linear(fl_context* ctx, int x_dtype, const void* x, int rows, int in_cols, int w_dtype,
+              const void* w, int w_layout, int out_cols, const void* bias, int act, int math,
+              void* out) {
   FL_ENTER(ctx);
-  if (!valid_dtype(dtype) || rows < 0 || in_cols <= 0 || out_cols <= 0 || !x || !w || !out)
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype) || rows < 0 || in_cols <= 0 ||
+      out_cols <= 0 || !x || !w || !out)
     return fail(FL_ERR_INVALID, "fl_linear: bad arguments");
   if (w_layout != FL_W_IN_OUT && w_layout != FL_W_OUT_IN)
     return fail(FL_ERR_INVALID, "fl_linear: bad weight layout");
   if (act < FL_ACT_IDENTITY || act > FL_ACT_SWIGLU) return fail(FL_ERR_INVALID, "bad activation");
   if (act == FL_ACT_SWIGLU && out_cols % 2) return fail(FL_ERR_INVALID, "SwiGLU needs even width");
+  // The result, the bias and the arithmetic follow the weight's type; x is
+  // converted to it (metal_darwin.go:806-829, 887-903).
+  const int dtype = w_dtype;
+  const size_t esz = dtype_size(dtype);
+  const int res_cols = act == FL_ACT_SWIGLU ? out_cols / 2 : out_cols;
+  FL_EXTENT(x, span(rows, in_cols, in_cols, x_dtype), "fl_linear x");
+  FL_EXTENT(w, span(in_cols, out_cols, out_cols, dtype), "fl_linear W");
+  if (bias) FL_EXTENT(bias, span(1, out_cols, out_cols, dtype), "fl_linear bias");
+  FL_EXTENT(out, span(rows, res_cols, res_cols, dtype), "fl_linear out");
   if (rows == 0) return FL_OK;
   note_write(ctx, out);
-  const size_t esz = dtype_size(dtype);
-  // Scratch layout: [fp32 bias][packed W][unfused product]
   const size_t bias_bytes = bias ? ((size_t)out_cols * 4 + 255) / 256 * 256 : 0;
   const size_t w_bytes = ((size_t)out_cols * in_cols * esz + 255) / 256 * 256;
   // SwiGLU runs in the four-wave kernel's epilogue when that kernel takes the
   // shape (16-bit, exact math); otherwise the full product is written first.
+  // (A converted x lies in a 256-byte aligned block.)
+  const uintptr_t x_addr = x_dtype != dtype ? 0 : (uintptr_t)x;
   const bool w_rows_ok =
       w_layout == FL_W_IN_OUT || !(((uintptr_t)w | ((size_t)in_cols * esz)) & 15);
   const bool fused_swiglu =
-      act == FL_ACT_SWIGLU && w_rows_ok && !(((uintptr_t)x | (uintptr_t)out) & 15) &&
+      act == FL_ACT_SWIGLU && w_rows_ok && !((x_addr | (uintptr_t)out) & 15) &&
       gemm_w4_layout(dtype, out_cols, in_cols, EPI_SWIGLU, math, bias != nullptr) >= 0;
   const bool unfused = (act == FL_ACT_SWIGLU && !fused_swiglu) || act == FL_ACT_SOFTMAX;
-  const size_t y_bytes = unfused ? (size_t)rows * out_cols * esz : 0;
+  const size_t y_bytes = unfused ? ((size_t)rows * out_cols * esz + 255) / 256 * 256 : 0;
+  const size_t xc_bytes = x_dtype != dtype ? (size_t)rows * in_cols * esz : 0;
   int st;
-  // [packed fp32 bias][fp32 bias staging][packed W][unfused product]
-  char* ws = (char*)workspace(ctx, 2 * bias_bytes + w_bytes + y_bytes, &st);
+  // [packed fp32 bias][fp32 bias staging][packed W][unfused product][x converted]
+  char* ws = (char*)workspace(ctx, 2 * bias_bytes + w_bytes + y_bytes + xc_bytes, &st);
   if (st) return st;
+  if (x_dtype != dtype) {
+    // x in the weight's type: a copy kept with the buffer like a packed
+    // weight, so the Q, K and V projections of one hidden state convert it
+    // once (and a LayerNorm that rewrites the buffer refreshes the copy in
+    // its own pass).
+    auto conv = [&](void* dst) {
+      return launch_cast(x, x_dtype, dst, dtype, (int64_t)rows * in_cols, 0, ctx->stream);
+    };
+    x = packed(ctx, {(uintptr_t)x, PK_CONVERTED, dtype, rows, in_cols, 0, x_dtype},
+               (size_t)rows * in_cols * esz, conv, ws + 2 * bias_bytes + w_bytes + y_bytes, &st);
+    if (st) return st;
+  }
   void* y = unfused ? (void*)(ws + 2 * bias_bytes + w_bytes) : out;
   const int epi_act = (act == FL_ACT_GELU || act == FL_ACT_TANH) ? act : FL_ACT_IDENTITY;
 
@@ -603,17 +658,21 @@ int fl_linear(fl_context* ctx, int dtype, const void* x, int rows, int in_cols, 
   return FL_OK;
 }
 
-int fl_add(fl_context* ctx, int dtype, void* t, const void* other, int64_t n) {
+int fl_add(fl_context* ctx, int dtype, void* t, int other_dtype, const void* other, int64_t n) {
   FL_ENTER(ctx);
-  if (!valid_dtype(dtype) || n < 0 || (n > 0 && (!t || !other))) return fail(FL_ERR_INVALID, "fl_add");
+  if (!valid_dtype(dtype) || !valid_dtype(other_dtype) || n < 0 || (n > 0 && (!t || !other)))
+    return fail(FL_ERR_INVALID, "fl_add");
+  FL_EXTENT(t, n * (int64_t)dtype_size(dtype), "fl_add t");
+  FL_EXTENT(other, n * (int64_t)dtype_size(other_dtype), "fl_add other");
   note_write(ctx, t);
-  FL_CHECK_LAUNCH(launch_add(dtype, t, other, n, ctx->stream));
+  FL_CHECK_LAUNCH(launch_add(dtype, t, other_dtype, other, n, ctx->stream));
   return FL_OK;
 }
 
 int fl_add_scalar(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_add_scalar");
+  FL_EXTENT(t, n * (int64_t)dtype_size(dtype), "fl_add_scalar t");
   note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_affine(dtype, t, n, 1.0f, v, ctx->stream));
   return FL_OK;
@@ -622,6 +681,7 @@ int fl_add_scalar(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
 int fl_scale(fl_context* ctx, int dtype, void* t, int64_t n, float v) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_scale");
+  FL_EXTENT(t, n * (int64_t)dtype_size(dtype), "fl_scale t");
   if (v == 1.0f) return FL_OK;
   note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_affine(dtype, t, n, v, 0.0f, ctx->stream));
@@ -632,6 +692,8 @@ int fl_add_bias(fl_context* ctx, int dtype, void* t, int rows, int cols, const v
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !bias)
     return fail(FL_ERR_INVALID, "fl_add_bias");
+  FL_EXTENT(t, span(rows, cols, cols, dtype), "fl_add_bias t");
+  FL_EXTENT(bias, span(1, cols, cols, dtype), "fl_add_bias bias");
   note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_add_bias(dtype, t, rows, cols, bias, ctx->stream));
   return FL_OK;
@@ -642,8 +704,38 @@ int fl_activation(fl_context* ctx, int dtype, void* t, int rows, int cols, int a
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t) return fail(FL_ERR_INVALID, "fl_activation");
   if (act != FL_ACT_GELU && act != FL_ACT_TANH && act != FL_ACT_SOFTMAX && act != FL_ACT_IDENTITY)
     return fail(FL_ERR_INVALID, "fl_activation: unsupported activation");
+  FL_EXTENT(t, span(rows, cols, cols, dtype), "fl_activation t");
   note_write(ctx, t);
   FL_CHECK_LAUNCH(launch_activation(dtype, t, rows, cols, act, math, ctx->stream));
+  return FL_OK;
+}
+
+// LayerNorm / AddLayerNorm over an fp32 receiver that a 16-bit Linear has
+// read (so a converted copy is kept): the kernel rewrites that copy in the
+// same pass, and it stays valid for the next Linear.
+static int layernorm_common(fl_context* ctx, int dtype, void* t, int res_dtype, const void* residual,
+                            int rows, int cols, const float* gamma, const float* beta, float eps) {
+  FL_EXTENT(t, span(rows, cols, cols, dtype), "LayerNorm t");
+  if (residual) FL_EXTENT(residual, span(rows, cols, cols, res_dtype), "AddLayerNorm residual");
+  FL_EXTENT(gamma, (int64_t)cols * 4, "LayerNorm gamma");
+  FL_EXTENT(beta, (int64_t)cols * 4, "LayerNorm beta");
+  fl_context::PackEntry* copy = nullptr;
+  int copy_dtype = FL_F16;
+  if (dtype == FL_F32) {
+    for (int cd : {FL_F16, FL_BF16}) {
+      copy = find_pack(ctx, {(uintptr_t)t, PK_CONVERTED, cd, rows, cols, 0, FL_F32});
+      if (copy) {
+        copy_dtype = cd;
+        break;
+      }
+    }
+  }
+  note_write(ctx, t);
+  FL_CHECK_LAUNCH(launch_layernorm_mixed(dtype, t, res_dtype, residual, rows, cols, gamma, beta,
+                                         eps, copy_dtype, copy ? copy->buf : nullptr,
+                                         ctx->stream));
+  if (copy)
+    if (const fl_context::Live* l = find_live(ctx, t)) copy->gen = l->gen;
   return FL_OK;
 }
 
@@ -653,20 +745,17 @@ int fl_layernorm(fl_context* ctx, int dtype, void* t, int rows, int cols, const 
   if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !gamma || !beta)
     return fail(FL_ERR_INVALID, "fl_layernorm");
   if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_layernorm: cols > 4096");
-  note_write(ctx, t);
-  FL_CHECK_LAUNCH(launch_layernorm(dtype, t, nullptr, rows, cols, gamma, beta, eps, ctx->stream));
-  return FL_OK;
+  return layernorm_common(ctx, dtype, t, dtype, nullptr, rows, cols, gamma, beta, eps);
 }
 
-int fl_add_layernorm(fl_context* ctx, int dtype, void* t, const void* residual, int rows, int cols,
-                     const float* gamma, const float* beta, float eps) {
+int fl_add_layernorm(fl_context* ctx, int dtype, void* t, int res_dtype, const void* residual,
+                     int rows, int cols, const float* gamma, const float* beta, float eps) {
   FL_ENTER(ctx);
-  if (!valid_dtype(dtype) || rows < 0 || cols <= 0 || !t || !residual || !gamma || !beta)
+  if (!valid_dtype(dtype) || !valid_dtype(res_dtype) || rows < 0 || cols <= 0 || !t ||
+      !residual || !gamma || !beta)
     return fail(FL_ERR_INVALID, "fl_add_layernorm");
   if (cols > 4096) return fail(FL_ERR_UNSUPPORTED, "fl_add_layernorm: cols > 4096");
-  note_write(ctx, t);
-  FL_CHECK_LAUNCH(launch_layernorm(dtype, t, residual, rows, cols, gamma, beta, eps, ctx->stream));
-  return FL_OK;
+  return layernorm_common(ctx, dtype, t, res_dtype, residual, rows, cols, gamma, beta, eps);
 }
 
 int fl_gather_rows(fl_context* ctx, int dtype, const void* table, int rows, int cols,
@@ -675,6 +764,8 @@ int fl_gather_rows(fl_context* ctx, int dtype, const void* table, int rows, int 
   if (!valid_dtype(dtype) || rows <= 0 || cols <= 0 || n < 0 || !table || (n > 0 && (!idx || !out)))
     return fail(FL_ERR_INVALID, "fl_gather_rows");
   if (n == 0) return FL_OK;
+  FL_EXTENT(table, span(rows, cols, cols, dtype), "Gather table");
+  FL_EXTENT(out, span(n, cols, cols, dtype), "Gather out");
   std::vector<int> i32(n);
   for (int i = 0; i < n; ++i) {
     // cpu_backend.go:500-502 panics on out-of-range indices.
@@ -695,6 +786,9 @@ static int rope_common(fl_context* ctx, int dtype, void* t, const std::vector<in
   if (head_dim % 2) return fail(FL_ERR_INVALID, "RoPE needs an even head_dim");
   const int rows = (int)pos.size();
   if (rows == 0) return FL_OK;
+  // cpu_backend.go:760-805 rotates batch * seq rows of the tensor (an index
+  // panic in Go when the tensor is shorter).
+  FL_EXTENT(t, span(rows, (int64_t)heads * head_dim, (int64_t)heads * head_dim, dtype), "ApplyRoPE t");
   int maxp = 0;
   for (int p : pos) maxp = p > maxp ? p : maxp;
   int st;
@@ -742,11 +836,19 @@ static int attention_common(fl_context* ctx, int dtype, const void* q, const voi
   const int hd = hidden / heads;
   std::vector<int> cu(nseq + 1, 0);
   int max_len = 0;
+  int64_t total = 0;
   for (int b = 0; b < nseq; ++b) {
     if (lengths[b] < 0) return fail(FL_ERR_INVALID, "negative length");
+    total += lengths[b];
+    if (total > INT32_MAX) return fail(FL_ERR_INVALID, "attention: too many rows");
     cu[b + 1] = cu[b] + (int)lengths[b];
     max_len = (int)lengths[b] > max_len ? (int)lengths[b] : max_len;
   }
+  const int64_t ext = span(total, hidden, hidden, dtype);
+  FL_EXTENT(q, ext, "Attention q");
+  FL_EXTENT(k, ext, "Attention k");
+  FL_EXTENT(v, ext, "Attention v");
+  FL_EXTENT(out, ext, "Attention out");
   const bool fast16 = (dtype == FL_F16 || dtype == FL_BF16) && (hd == 64 || hd == 32) &&
                       math == FL_MATH_EXACT &&
                       hidden % 8 == 0 && (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0 &&
@@ -815,6 +917,8 @@ int fl_cast(fl_context* ctx, const void* src, int src_dtype, void* dst, int dst_
   FL_ENTER(ctx);
   if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype) || n < 0 || (n > 0 && (!src || !dst)))
     return fail(FL_ERR_INVALID, "fl_cast");
+  FL_EXTENT(src, n * (int64_t)dtype_size(src_dtype), "Cast src");
+  FL_EXTENT(dst, n * (int64_t)dtype_size(dst_dtype), "Cast dst");
   note_write(ctx, dst);
   FL_CHECK_LAUNCH(launch_cast(src, src_dtype, dst, dst_dtype, n, 0, ctx->stream));
   return FL_OK;
@@ -823,6 +927,7 @@ int fl_cast(fl_context* ctx, const void* src, int src_dtype, void* dst, int dst_
 int fl_has_nan(fl_context* ctx, const void* t, int dtype, int64_t n, int* out) {
   FL_ENTER(ctx);
   if (!valid_dtype(dtype) || n < 0 || !out || (n > 0 && !t)) return fail(FL_ERR_INVALID, "fl_has_nan");
+  FL_EXTENT(t, n * (int64_t)dtype_size(dtype), "HasNaN t");
   FL_CHECK_LAUNCH(hipMemsetAsync(ctx->flag, 0, 4, ctx->stream));
   FL_CHECK_LAUNCH(launch_has_nan(t, dtype, n, ctx->flag, ctx->stream));
   int h = 0;
@@ -839,6 +944,8 @@ int fl_slice(fl_context* ctx, int dtype, const void* src, int rows, int cols, in
   if (!valid_dtype(dtype) || !src || !dst || r0 < 0 || c0 < 0 || r1 > rows || c1 > cols ||
       r1 - r0 <= 0 || c1 - c0 <= 0)
     return fail(FL_ERR_INVALID, "Slice: invalid dimensions");
+  FL_EXTENT(src, span(rows, cols, cols, dtype), "Slice src");
+  FL_EXTENT(dst, span(r1 - r0, c1 - c0, c1 - c0, dtype), "Slice dst");
   note_write(ctx, dst);
   FL_CHECK_LAUNCH(launch_slice(dtype, src, cols, r0, r1, c0, c1, dst, ctx->stream));
   return FL_OK;
@@ -852,11 +959,16 @@ int fl_mean_pool(fl_context* ctx, int dtype, const void* hidden, int cols, const
   if (nseq == 0) return FL_OK;
   std::vector<int> cu(nseq + 1, 0);
   int max_len = 0;
+  int64_t total = 0;
   for (int b = 0; b < nseq; ++b) {
     if (lengths[b] <= 0) return fail(FL_ERR_INVALID, "mean pool needs non-empty sequences");
+    total += lengths[b];
+    if (total > INT32_MAX) return fail(FL_ERR_INVALID, "fl_mean_pool: too many rows");
     cu[b + 1] = cu[b] + (int)lengths[b];
     max_len = (int)lengths[b] > max_len ? (int)lengths[b] : max_len;
   }
+  FL_EXTENT(hidden, span(cu[nseq], cols, cols, dtype), "mean pool hidden");
+  FL_EXTENT(out, span(nseq, cols, cols, FL_F32), "mean pool out");
   const int rpc = 64;
   const size_t chunks = (size_t)(max_len + rpc - 1) / rpc;
   const size_t cu_bytes = ((size_t)(nseq + 1) * 4 + 255) / 256 * 256;
@@ -897,6 +1009,8 @@ int fl_mean_pool_noalloc(fl_context* ctx, int dtype, const void* hidden, int col
                                     std::to_string(need) + " bytes, the scratch array holds " +
                                     std::to_string((int64_t)FL_NOALLOC_PARTIAL_BYTES));
   if (!ctx->noalloc) return fail(FL_ERR_HIP, "fl_mean_pool_noalloc: no scratch address");
+  FL_EXTENT(hidden, span(total, cols, cols, dtype), "mean pool hidden");
+  FL_EXTENT(out, span(nseq, cols, cols, FL_F32), "mean pool out");
   note_write(ctx, out);
   FL_CHECK_LAUNCH(launch_mean_pool_noalloc(dtype, hidden, cols, la, max_len, l2, out,
                                            ctx->noalloc, ctx->stream));

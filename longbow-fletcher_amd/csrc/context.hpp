@@ -31,10 +31,13 @@ struct fl_context {
   // cached, workspace, tables, model buffers.
   int64_t allocated = 0;
 
-  // fl_alloc buffers in use, by base address: size class, device, and the
-  // write generation (bumped by every entry point that writes into it).
+  // fl_alloc buffers in use, by base address: size class, the bytes asked
+  // for (the extent every per-op entry point checks its operands against),
+  // device, and the write generation (bumped by every entry point that writes
+  // into it).
   struct Live {
     size_t cls = 0;
+    size_t bytes = 0;
     int device = 0;
     uint64_t gen = 0;
   };
@@ -45,8 +48,10 @@ struct fl_context {
   int64_t cached_bytes = 0;
   int64_t pool_hits = 0, pool_misses = 0;
 
-  // Packed weights of fl_linear / fl_gemm, keyed by the source pointer and
-  // how it was packed; valid while the source buffer's generation matches.
+  // Packed weights of fl_linear / fl_gemm, and converted copies of
+  // activations (an fp32 tensor read by a 16-bit Linear), keyed by the source
+  // pointer and how it was packed; valid while the source buffer's generation
+  // matches.
   struct PackKey {
     uintptr_t src;
     int kind, dtype, rows, cols, layout, extra;
@@ -112,6 +117,12 @@ void* workspace(fl_context* ctx, size_t bytes, int* status);
 // p < max_pos: angles and products in float64, cast to float32 once.
 const float2* rope_table(fl_context* ctx, float base, int half, int max_pos, int* status,
                          float scale = 1.0f);
+// hipMalloc that, when the device is full, waits for the context stream,
+// gives the cached blocks back (and, with evict_packs, the packed weights and
+// converted activations) and tries once more.  Every device allocation of the
+// library goes through it.  evict_packs must be false while the caller holds
+// a pointer from cached_pack.
+hipError_t malloc_retry(fl_context* ctx, void** out, size_t bytes, bool evict_packs = true);
 // hipMalloc / hipFree counted in ctx->allocated (fl_vram_usage).
 int device_alloc(fl_context* ctx, size_t bytes, void** out);
 void device_free(fl_context* ctx, void* p, size_t bytes);
@@ -121,21 +132,30 @@ constexpr int64_t kPackCacheLimit = (int64_t)8 << 30;  // packed weights kept at
 constexpr size_t kStageMax = (size_t)64 << 20;          // larger uploads are synchronous
 size_t pool_class(size_t bytes);
 // A block of at least `bytes` on the current device (not zeroed): a cached
-// one when available, else hipMalloc (after giving cached blocks back if the
-// device is full).
-int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls);
+// one when available, else malloc_retry.
+int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls, bool evict_packs = true);
 void pool_put(fl_context* ctx, void* p, size_t cls, int device);
 // hipFree of every cached block.
 void pool_trim(fl_context* ctx);
-// The fl_alloc buffer containing ptr, or null.
-fl_context::Live* find_live(fl_context* ctx, const void* ptr);
+// hipFree of every packed weight and converted activation (the stream must be idle).
+void drop_all_packs(fl_context* ctx);
+// The fl_alloc buffer containing ptr (base address in *base), or null.
+fl_context::Live* find_live(fl_context* ctx, const void* ptr, uintptr_t* base = nullptr);
+// FL_OK when [ptr, ptr + bytes) lies inside the fl_alloc buffer that holds
+// ptr, or when ptr is not inside any fl_alloc buffer of the context (memory
+// of another allocator, which the library cannot size); FL_ERR_INVALID
+// naming `what` when the operand runs past the end of its buffer.
+int check_extent(fl_context* ctx, const void* ptr, int64_t bytes, const char* what);
+// The cache entry of key, or null (no packing, no generation check).
+fl_context::PackEntry* find_pack(fl_context* ctx, const fl_context::PackKey& key);
 // Marks the fl_alloc buffer containing ptr (if any) as written.
 void note_write(fl_context* ctx, const void* ptr);
 // Releases the packed copies of sources inside [base, base + cls).
 void drop_packs(fl_context* ctx, uintptr_t base, size_t cls);
 // The packed form of key.src (an fl_alloc buffer), made by pack(dst) when
 // missing or when the source was written since; null when the source is not
-// an fl_alloc buffer or the cache is full (the caller packs into scratch).
+// an fl_alloc buffer or the cache is full or the device has no room for it
+// (the caller packs into scratch).
 const void* cached_pack(fl_context* ctx, const fl_context::PackKey& key, size_t bytes,
                         const std::function<hipError_t(void*)>& pack, int* status);
 // Host -> device copy on the context stream that returns without waiting:

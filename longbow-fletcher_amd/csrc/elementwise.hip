@@ -20,10 +20,12 @@ static inline dim3 grid_for(int64_t n, int per_block = 256 * 4) {
 #define FL_GRID_STRIDE(i, n) \
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < (n); i += (int64_t)gridDim.x * blockDim.x)
 
-template <typename T>
-__global__ void add_kernel(T* t, const T* o, int64_t n) {
+// t += o: the other operand takes the receiver's type (Tensor.Add,
+// metal_darwin.go:603-619), converted on load.
+template <typename T, typename O>
+__global__ void add_kernel(T* t, const O* o, int64_t n) {
 #pragma clang fp contract(off)
-  FL_GRID_STRIDE(i, n) t[i] = from_f<T>(to_f(t[i]) + to_f(o[i]));
+  FL_GRID_STRIDE(i, n) t[i] = from_f<T>(to_f(t[i]) + to_f(from_f<T>(to_f(o[i]))));
 }
 
 template <typename T>
@@ -355,10 +357,11 @@ __global__ void untile_kernel(const T* in, int64_t rows, int cols, T* out) {
     default: return hipErrorInvalidValue;       \
   }
 
-hipError_t launch_add(int dtype, void* t, const void* o, int64_t n, hipStream_t s) {
+hipError_t launch_add(int dtype, void* t, int odtype, const void* o, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  FL_DISPATCH(dtype, T, hipLaunchKernelGGL(add_kernel<T>, grid_for(n), dim3(256), 0, s, (T*)t,
-                                           (const T*)o, n));
+  FL_DISPATCH(dtype, T, FL_DISPATCH(odtype, O, hipLaunchKernelGGL((add_kernel<T, O>), grid_for(n),
+                                                                  dim3(256), 0, s, (T*)t,
+                                                                  (const O*)o, n)));
   return hipGetLastError();
 }
 

@@ -197,6 +197,13 @@ hipError_t launch_attention_generic(int dtype, const void* q, const void* k, con
 hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, int cols,
                             const float* gamma, const float* beta, float eps,
                             hipStream_t stream, bool t_tiled = false, int ld_res = 0);
+// t = LN(t [+ residual]) over row-major [rows, cols] for the per-op ABI: the
+// residual in its own storage type (res_dtype, converted on load); with
+// `shadow` (fp32 t only) the result is also stored as shadow_dtype (16-bit)
+// into shadow [rows, cols] in the same pass.
+hipError_t launch_layernorm_mixed(int dtype, void* t, int res_dtype, const void* residual,
+                                  int rows, int cols, const float* gamma, const float* beta,
+                                  float eps, int shadow_dtype, void* shadow, hipStream_t stream);
 // x[t] = LN(word[ids[t]] + pos[pos_ids[t]] (if pos) + type[0]).  Ids outside
 // [0, vocab) read row 0 and set *bad_id (never an out-of-bounds read).
 hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const void* word,
@@ -205,7 +212,8 @@ hipError_t launch_embed_ln(int dtype, const int* ids, const int* pos_ids, const 
                            int* bad_id, void* out, hipStream_t stream, bool out_tiled = false);
 
 // ---- elementwise ------------------------------------------------------------
-hipError_t launch_add(int dtype, void* t, const void* o, int64_t n, hipStream_t s);
+// t += o, o stored as odtype and converted to t's type on load.
+hipError_t launch_add(int dtype, void* t, int odtype, const void* o, int64_t n, hipStream_t s);
 hipError_t launch_affine(int dtype, void* t, int64_t n, float mul, float add, hipStream_t s);
 hipError_t launch_add_bias(int dtype, void* t, int rows, int cols, const void* bias,
                            hipStream_t s);

@@ -7,6 +7,8 @@
 // (cpu_backend.go:603-610) adds the residual first.  One wave per row: a
 // row of H = 768 is 12 values per lane held in registers, so every element is
 // read once and written once.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -115,15 +117,20 @@ __device__ inline void ln_core(float (&x)[NCH][VEC], const bool (&valid)[NCH], i
         x[c][i] = (x[c][i] - mean) * inv * gamma[col0[c] + i] + beta[col0[c] + i];
 }
 
-template <typename T, int NCH, int VEC>
+// R: the residual branch's storage type (converted on load, Tensor.Add's
+// rule: the branch takes the receiver's type).  S: when it differs from T
+// (an fp32 receiver), the normalised row is also stored as S into `shadow`,
+// the 16-bit copy a following 16-bit Linear reads, in the same pass.
+template <typename T, typename R, typename S, int NCH, int VEC>
 __global__ void __launch_bounds__(256)
-layernorm_kernel(T* t, const T* residual, int ldr, int rows, int cols, const float* gamma,
-                 const float* beta, float eps) {
+layernorm_kernel(T* t, const R* residual, int ldr, int rows, int cols, const float* gamma,
+                 const float* beta, float eps, S* shadow) {
+  constexpr bool SH = !std::is_same<S, T>::value;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   T* tr = t + (size_t)row * cols;
-  const T* rr = residual ? residual + (size_t)row * ldr : nullptr;
+  const R* rr = residual ? residual + (size_t)row * ldr : nullptr;
   float x[NCH][VEC];
   bool valid[NCH];
   int col0[NCH];
@@ -135,7 +142,7 @@ layernorm_kernel(T* t, const T* residual, int ldr, int rows, int cols, const flo
       load_vec<T, VEC>(tr + col0[c], x[c]);
       if (rr) {
         float r[VEC];
-        load_vec<T, VEC>(rr + col0[c], r);
+        load_vec<R, VEC>(rr + col0[c], r);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + r[i];
       }
@@ -144,7 +151,10 @@ layernorm_kernel(T* t, const T* residual, int ldr, int rows, int cols, const flo
   ln_core<NCH, VEC>(x, valid, cols, gamma, beta, col0, eps);
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    if (valid[c]) store_vec<T, VEC>(tr + col0[c], x[c]);
+    if (valid[c]) {
+      store_vec<T, VEC>(tr + col0[c], x[c]);
+      if constexpr (SH) store_vec<S, VEC>(shadow + (size_t)row * cols + col0[c], x[c]);
+    }
 }
 
 // 16-byte vectors, LPR lanes per row (64 / LPR rows per wave): for H = 768
@@ -153,15 +163,16 @@ layernorm_kernel(T* t, const T* residual, int ldr, int rows, int cols, const flo
 // TT: t is stored tiled (tiled_act_offset), 16-byte vectors never straddle
 // a tiled chunk; the two rows of a wave are adjacent, so each load of the
 // wave covers whole 128-byte lines of the tiled blocks.
-template <typename T, int LPR, int NCH, int VEC, bool TT>
+template <typename T, typename R, typename S, int LPR, int NCH, int VEC, bool TT>
 __global__ void __launch_bounds__(256)
-layernorm_rows_kernel(T* t, const T* residual, int ldr, int rows, int cols, const float* gamma,
-                      const float* beta, float eps) {
+layernorm_rows_kernel(T* t, const R* residual, int ldr, int rows, int cols, const float* gamma,
+                      const float* beta, float eps, S* shadow) {
+  constexpr bool SH = !std::is_same<S, T>::value;
   constexpr int RPW = 64 / LPR;
   const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + ((threadIdx.x & 63) / LPR);
   const int lane = threadIdx.x % LPR;
   if (row >= rows) return;
-  const T* rr = residual ? residual + (size_t)row * ldr : nullptr;
+  const R* rr = residual ? residual + (size_t)row * ldr : nullptr;
   float x[NCH][VEC];
   bool valid[NCH];
   int col0[NCH];
@@ -180,7 +191,7 @@ layernorm_rows_kernel(T* t, const T* residual, int ldr, int rows, int cols, cons
     for (int c = 0; c < NCH; ++c)
       if (valid[c]) {
         float r[VEC];
-        load_vec_once<T, VEC>(rr + col0[c], r);
+        load_vec_once<R, VEC>(rr + col0[c], r);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) x[c][i] = x[c][i] + r[i];
       }
@@ -188,65 +199,82 @@ layernorm_rows_kernel(T* t, const T* residual, int ldr, int rows, int cols, cons
   ln_core<NCH, VEC, LPR>(x, valid, cols, gamma, beta, col0, eps);
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
-    if (valid[c]) store_vec<T, VEC>(tp(col0[c]), x[c]);
+    if (valid[c]) {
+      store_vec<T, VEC>(tp(col0[c]), x[c]);
+      if constexpr (SH) store_vec<S, VEC>(shadow + (size_t)row * cols + col0[c], x[c]);
+    }
 }
 
-template <typename T, int LPR, int NCH, int VEC>
+template <typename T, typename R, typename S, int LPR, int NCH, int VEC>
 static hipError_t ln_rows_launch(void* t, const void* res, int ldr, int rows, int cols,
                                  const float* g, const float* b, float eps, hipStream_t s,
-                                 bool tiled) {
+                                 bool tiled, void* shadow) {
   constexpr int rows_per_block = 4 * (64 / LPR);
   const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
-  if (tiled)
-    hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, true>), grid, dim3(256), 0, s,
-                       (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
-  else
-    hipLaunchKernelGGL((layernorm_rows_kernel<T, LPR, NCH, VEC, false>), grid, dim3(256), 0, s,
-                       (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
+  if constexpr (std::is_same<R, T>::value && std::is_same<S, T>::value) {
+    if (tiled) {
+      hipLaunchKernelGGL((layernorm_rows_kernel<T, R, S, LPR, NCH, VEC, true>), grid, dim3(256),
+                         0, s, (T*)t, (const R*)res, ldr, rows, cols, g, b, eps, (S*)shadow);
+      return hipGetLastError();
+    }
+  } else {
+    if (tiled) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((layernorm_rows_kernel<T, R, S, LPR, NCH, VEC, false>), grid, dim3(256), 0,
+                     s, (T*)t, (const R*)res, ldr, rows, cols, g, b, eps, (S*)shadow);
   return hipGetLastError();
 }
 
-template <typename T, int NCH, int VEC>
+template <typename T, typename R, typename S, int NCH, int VEC>
 static hipError_t ln_launch(void* t, const void* res, int ldr, int rows, int cols, const float* g,
-                            const float* b, float eps, hipStream_t s) {
-  hipLaunchKernelGGL((layernorm_kernel<T, NCH, VEC>), dim3((rows + 3) / 4), dim3(256), 0, s,
-                     (T*)t, (const T*)res, ldr, rows, cols, g, b, eps);
+                            const float* b, float eps, hipStream_t s, void* shadow) {
+  hipLaunchKernelGGL((layernorm_kernel<T, R, S, NCH, VEC>), dim3((rows + 3) / 4), dim3(256), 0,
+                     s, (T*)t, (const R*)res, ldr, rows, cols, g, b, eps, (S*)shadow);
   return hipGetLastError();
 }
 
 // ldr: row stride of the residual (elements).
-template <typename T>
+template <typename T, typename R, typename S>
 static hipError_t ln_typed(void* t, const void* res, int ldr, int rows, int cols,
-                           const float* g, const float* b, float eps, hipStream_t s, bool tiled) {
+                           const float* g, const float* b, float eps, hipStream_t s, bool tiled,
+                           void* shadow) {
   constexpr int V16 = 16 / sizeof(T);  // elements per 16-byte vector
-  const bool a16 = (((uintptr_t)t | (uintptr_t)res | ((size_t)ldr * sizeof(T))) % 16) == 0;
+  // Every operand's vectors aligned: V16 elements of T, of R and of S.
+  auto aligned = [&](size_t vec) {
+    return (((uintptr_t)t | (uintptr_t)res | (uintptr_t)shadow) % 16 == 0) &&
+           ((size_t)ldr * sizeof(R)) % (vec * sizeof(R)) == 0 &&
+           (uintptr_t)res % (vec * sizeof(R)) == 0 && (uintptr_t)shadow % (vec * sizeof(S)) == 0;
+  };
+  const bool a16 = aligned(V16);
   if (cols % (32 * V16) == 0 && cols <= 4 * 32 * V16 && a16) {
     switch (cols / (32 * V16)) {
-      case 1: return ln_rows_launch<T, 32, 1, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
-      case 2: return ln_rows_launch<T, 32, 2, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
-      case 3: return ln_rows_launch<T, 32, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
-      case 4: return ln_rows_launch<T, 32, 4, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled);
+      case 1: return ln_rows_launch<T, R, S, 32, 1, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled, shadow);
+      case 2: return ln_rows_launch<T, R, S, 32, 2, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled, shadow);
+      case 3: return ln_rows_launch<T, R, S, 32, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled, shadow);
+      case 4: return ln_rows_launch<T, R, S, 32, 4, V16>(t, res, ldr, rows, cols, g, b, eps, s, tiled, shadow);
     }
   }
   // Widths of 3 x 16 vectors (384 in 16 bits: MiniLM): 16 lanes per row.
   if (sizeof(T) == 2 && !tiled && cols == 3 * 16 * V16 && a16)
-    return ln_rows_launch<T, 16, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, false);
+    return ln_rows_launch<T, R, S, 16, 3, V16>(t, res, ldr, rows, cols, g, b, eps, s, false,
+                                               shadow);
   if (tiled) return hipErrorInvalidValue;
-  if (cols % 4 == 0 && (((uintptr_t)t | (uintptr_t)res | ((size_t)ldr * sizeof(T))) %
-                        (4 * sizeof(T))) == 0) {
+  if (cols % 4 == 0 && ((uintptr_t)t % (4 * sizeof(T))) == 0 &&
+      ((uintptr_t)shadow % (4 * sizeof(S))) == 0 && ((uintptr_t)res % (4 * sizeof(R))) == 0 &&
+      ((size_t)ldr % 4) == 0) {
     const int nch = (cols / 4 + 63) / 64;
-    if (nch <= 1) return ln_launch<T, 1, 4>(t, res, ldr, rows, cols, g, b, eps, s);
-    if (nch <= 2) return ln_launch<T, 2, 4>(t, res, ldr, rows, cols, g, b, eps, s);
-    if (nch <= 3) return ln_launch<T, 3, 4>(t, res, ldr, rows, cols, g, b, eps, s);
-    if (nch <= 4) return ln_launch<T, 4, 4>(t, res, ldr, rows, cols, g, b, eps, s);
-    if (nch <= 8) return ln_launch<T, 8, 4>(t, res, ldr, rows, cols, g, b, eps, s);
-    if (nch <= 16) return ln_launch<T, 16, 4>(t, res, ldr, rows, cols, g, b, eps, s);
+    if (nch <= 1) return ln_launch<T, R, S, 1, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+    if (nch <= 2) return ln_launch<T, R, S, 2, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+    if (nch <= 3) return ln_launch<T, R, S, 3, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+    if (nch <= 4) return ln_launch<T, R, S, 4, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+    if (nch <= 8) return ln_launch<T, R, S, 8, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+    if (nch <= 16) return ln_launch<T, R, S, 16, 4>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
     return hipErrorInvalidValue;
   }
   const int nch = (cols + 63) / 64;
-  if (nch <= 2) return ln_launch<T, 2, 1>(t, res, ldr, rows, cols, g, b, eps, s);
-  if (nch <= 8) return ln_launch<T, 8, 1>(t, res, ldr, rows, cols, g, b, eps, s);
-  if (nch <= 32) return ln_launch<T, 32, 1>(t, res, ldr, rows, cols, g, b, eps, s);
+  if (nch <= 2) return ln_launch<T, R, S, 2, 1>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+  if (nch <= 8) return ln_launch<T, R, S, 8, 1>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
+  if (nch <= 32) return ln_launch<T, R, S, 32, 1>(t, res, ldr, rows, cols, g, b, eps, s, shadow);
   return hipErrorInvalidValue;
 }
 
@@ -259,12 +287,62 @@ hipError_t launch_layernorm(int dtype, void* t, const void* residual, int rows, 
   if (ld_res < cols) return hipErrorInvalidValue;
   switch (dtype) {
     case F32:
-      return ln_typed<float>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream, false);
+      return ln_typed<float, float, float>(t, residual, ld_res, rows, cols, gamma, beta, eps,
+                                           stream, false, nullptr);
     case F16:
-      return ln_typed<_Float16>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream,
-                                t_tiled);
+      return ln_typed<_Float16, _Float16, _Float16>(t, residual, ld_res, rows, cols, gamma, beta,
+                                                    eps, stream, t_tiled, nullptr);
     case BF16:
-      return ln_typed<__bf16>(t, residual, ld_res, rows, cols, gamma, beta, eps, stream, t_tiled);
+      return ln_typed<__bf16, __bf16, __bf16>(t, residual, ld_res, rows, cols, gamma, beta, eps,
+                                              stream, t_tiled, nullptr);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T, typename R>
+static hipError_t ln_mixed_shadow(void* t, const void* res, int rows, int cols, const float* g,
+                                  const float* b, float eps, hipStream_t s, int sdtype,
+                                  void* shadow) {
+  if (!shadow) return ln_typed<T, R, T>(t, res, cols, rows, cols, g, b, eps, s, false, nullptr);
+  if constexpr (std::is_same<T, float>::value) {
+    if (sdtype == F16)
+      return ln_typed<T, R, _Float16>(t, res, cols, rows, cols, g, b, eps, s, false, shadow);
+    if (sdtype == BF16)
+      return ln_typed<T, R, __bf16>(t, res, cols, rows, cols, g, b, eps, s, false, shadow);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+static hipError_t ln_mixed_res(void* t, int rdtype, const void* res, int rows, int cols,
+                               const float* g, const float* b, float eps, hipStream_t s,
+                               int sdtype, void* shadow) {
+  if (!res) rdtype = Elem<T>::dtype;
+  switch (rdtype) {
+    case F32: return ln_mixed_shadow<T, float>(t, res, rows, cols, g, b, eps, s, sdtype, shadow);
+    case F16:
+      return ln_mixed_shadow<T, _Float16>(t, res, rows, cols, g, b, eps, s, sdtype, shadow);
+    case BF16:
+      return ln_mixed_shadow<T, __bf16>(t, res, rows, cols, g, b, eps, s, sdtype, shadow);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_layernorm_mixed(int dtype, void* t, int res_dtype, const void* residual,
+                                  int rows, int cols, const float* gamma, const float* beta,
+                                  float eps, int shadow_dtype, void* shadow, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (shadow && dtype != F32) return hipErrorInvalidValue;
+  switch (dtype) {
+    case F32:
+      return ln_mixed_res<float>(t, res_dtype, residual, rows, cols, gamma, beta, eps, stream,
+                                 shadow_dtype, shadow);
+    case F16:
+      return ln_mixed_res<_Float16>(t, res_dtype, residual, rows, cols, gamma, beta, eps, stream,
+                                    shadow_dtype, nullptr);
+    case BF16:
+      return ln_mixed_res<__bf16>(t, res_dtype, residual, rows, cols, gamma, beta, eps, stream,
+                                  shadow_dtype, nullptr);
   }
   return hipErrorInvalidValue;
 }

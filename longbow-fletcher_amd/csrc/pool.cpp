@@ -15,6 +15,7 @@
 // enqueued on the same stream behind the work that used it before.
 #include <algorithm>
 #include <cstring>
+#include <string>
 
 #include "context.hpp"
 
@@ -30,7 +31,24 @@ size_t pool_class(size_t bytes) {
   return (bytes + g - 1) / g * g;
 }
 
-int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls_out) {
+hipError_t malloc_retry(fl_context* ctx, void** out, size_t bytes, bool evict_packs) {
+  *out = nullptr;
+  hipError_t e = hipMalloc(out, bytes ? bytes : 16);
+  if (e != hipErrorOutOfMemory) return e;
+  // The device is full: clear the error, wait until the stream no longer
+  // uses the cached blocks, give them back (and the packed copies when the
+  // caller holds none) and try once more.
+  (void)hipGetLastError();
+  e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return e;
+  pool_trim(ctx);
+  if (evict_packs) drop_all_packs(ctx);
+  e = hipMalloc(out, bytes ? bytes : 16);
+  if (e == hipErrorOutOfMemory) (void)hipGetLastError();
+  return e;
+}
+
+int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls_out, bool evict_packs) {
   *out = nullptr;
   const size_t cls = pool_class(bytes);
   // A cached block of this class or up to two classes larger (like the
@@ -50,15 +68,7 @@ int pool_get(fl_context* ctx, size_t bytes, void** out, size_t* cls_out) {
   }
   ++ctx->pool_misses;
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, cls);
-  if (e == hipErrorOutOfMemory) {
-    // Give the cached blocks of this device back and try once more.
-    (void)hipGetLastError();
-    e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    pool_trim(ctx);
-    e = hipMalloc(&p, cls);
-  }
+  hipError_t e = malloc_retry(ctx, &p, cls, evict_packs);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(pool)");
   ctx->allocated += (int64_t)cls;
   *out = p;
@@ -82,13 +92,27 @@ void pool_trim(fl_context* ctx) {
   ctx->cached.clear();
 }
 
-fl_context::Live* find_live(fl_context* ctx, const void* ptr) {
+fl_context::Live* find_live(fl_context* ctx, const void* ptr, uintptr_t* base) {
   const uintptr_t a = (uintptr_t)ptr;
   auto it = ctx->live.upper_bound(a);
   if (it == ctx->live.begin()) return nullptr;
   --it;
   if (a >= it->first + it->second.cls) return nullptr;
+  if (base) *base = it->first;
   return &it->second;
+}
+
+int check_extent(fl_context* ctx, const void* ptr, int64_t bytes, const char* what) {
+  if (bytes <= 0 || !ptr) return FL_OK;
+  uintptr_t base = 0;
+  const fl_context::Live* l = find_live(ctx, ptr, &base);
+  if (!l) return FL_OK;
+  const uint64_t off = (uintptr_t)ptr - base;
+  if (off + (uint64_t)bytes <= l->bytes) return FL_OK;
+  return fail(FL_ERR_INVALID, std::string(what) + ": operand of " + std::to_string(bytes) +
+                                  " bytes at offset " + std::to_string(off) +
+                                  " runs past the end of its " + std::to_string(l->bytes) +
+                                  "-byte buffer");
 }
 
 void note_write(fl_context* ctx, const void* ptr) {
@@ -102,6 +126,23 @@ void drop_packs(fl_context* ctx, uintptr_t base, size_t cls) {
     ctx->pack_bytes -= (int64_t)it->second.cls;
     it = ctx->packs.erase(it);
   }
+}
+
+void drop_all_packs(fl_context* ctx) {
+  for (auto& kv : ctx->packs) {
+    (void)hipSetDevice(kv.second.device);
+    (void)hipFree(kv.second.buf);
+    ctx->allocated -= (int64_t)kv.second.cls;
+  }
+  (void)hipSetDevice(ctx->device);
+  ctx->packs.clear();
+  ctx->pack_bytes = 0;
+}
+
+fl_context::PackEntry* find_pack(fl_context* ctx, const fl_context::PackKey& key) {
+  auto it = ctx->packs.find(key);
+  if (it == ctx->packs.end() || it->second.device != ctx->device) return nullptr;
+  return &it->second;
 }
 
 const void* cached_pack(fl_context* ctx, const fl_context::PackKey& key, size_t bytes,
@@ -131,7 +172,18 @@ const void* cached_pack(fl_context* ctx, const fl_context::PackKey& key, size_t 
   if (ctx->pack_bytes + (int64_t)bytes > kPackCacheLimit) return nullptr;
   void* buf = nullptr;
   size_t cls = 0;
-  if ((*status = pool_get(ctx, bytes, &buf, &cls))) return nullptr;
+  // The caller may already hold another entry of this cache (a weight while
+  // its bias is packed): no eviction of packs here, and a full device only
+  // means this copy is not kept (the caller packs into its scratch).
+  const int st = pool_get(ctx, bytes, &buf, &cls, false);
+  if (st == FL_ERR_OOM) {
+    set_error("");
+    return nullptr;
+  }
+  if (st) {
+    *status = st;
+    return nullptr;
+  }
   hipError_t e = pack(buf);
   if (e != hipSuccess) {
     pool_put(ctx, buf, cls, ctx->device);
