@@ -255,9 +255,12 @@ int fl_mean_pool(fl_context *ctx, int dtype, const void *hidden, int cols,
  * each GPU the library runs on holds until the process ends.  Limits (else
  * FL_ERR_INVALID): nseq <= FL_NOALLOC_MAX_SEQS and
  * nseq * ceil(max(lengths) / 64) * cols * 4 <= FL_NOALLOC_PARTIAL_BYTES.
- * Every call on one GPU shares that GPU's array: calls of one context are
- * ordered on its stream, but calls that overlap on one GPU (several contexts
- * or streams at once) race. */
+ * Every call on one GPU shares that GPU's array.  Calls run in the order
+ * they are made: calls of one context are ordered on its stream, and a call
+ * from another context's stream first waits for the previous call's kernels
+ * (an event, no allocation).  Calls recorded under graph capture are not
+ * ordered against other streams: graphs that contain this call and run on
+ * one GPU at the same time race on the array. */
 #define FL_NOALLOC_MAX_SEQS 512
 #define FL_NOALLOC_PARTIAL_BYTES (16 << 20)
 int fl_mean_pool_noalloc(fl_context *ctx, int dtype, const void *hidden, int cols,
@@ -351,7 +354,9 @@ int fl_model_embed_ex(fl_model *model, const int64_t *ids, const int64_t *length
  * the pooling kernel, embeddings.go:757-764) and whether any id was outside
  * [0, vocab) (such ids read row 0).  Synchronises. */
 int fl_model_status(fl_model *model, int *nan_in_output, int *bad_ids);
-/* Last hidden states [sum(lengths) x hidden] of the previous forward, as fp32 on the host. */
+/* Last hidden states [sum(lengths) x hidden] of the previous forward, as fp32
+ * on the host.  After fl_model_embed: its plan's last forward (the batches
+ * computed together last). */
 int fl_model_last_hidden(fl_model *model, float *out, int64_t n);
 /* Kernel timing with HIP events on the context stream.  While enabled every
  * kernel of the forward is bracketed by events; fl_model_profile_read

@@ -1013,7 +1013,7 @@ int fl_mean_pool_noalloc(fl_context* ctx, int dtype, const void* hidden, int col
   FL_EXTENT(out, span(nseq, cols, cols, FL_F32), "mean pool out");
   note_write(ctx, out);
   FL_CHECK_LAUNCH(launch_mean_pool_noalloc(dtype, hidden, cols, la, max_len, l2, out,
-                                           ctx->noalloc, ctx->stream));
+                                           ctx->device, ctx->noalloc, ctx->stream));
   return FL_OK;
 }
 

@@ -535,6 +535,12 @@ static __device__ __align__(256) char scratch[kNoAllocCuBytes + FL_NOALLOC_PARTI
 constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
+// Per device: an event recorded after the last call's kernels and the stream
+// they ran on.  A call from another stream (another context on the same GPU)
+// waits for that event first, so calls of several contexts one after the
+// other do not overwrite each other's cu_seqlens and partial sums.
+static hipEvent_t g_scratch_done[kMaxDevices];
+static hipStream_t g_scratch_stream[kMaxDevices];
 
 hipError_t noalloc_scratch(int device, void** out) {
   *out = nullptr;
@@ -551,9 +557,38 @@ hipError_t noalloc_scratch(int device, void** out) {
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
+    // The ordering event (no device memory), made here with the address.
+    e = hipEventCreateWithFlags(&g_scratch_done[device], hipEventDisableTiming);
+    if (e != hipSuccess) return e;
     g_scratch_ptr[device] = p;
   }
   *out = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+// The array's address on `device` (set up by noalloc_scratch) must be what
+// scratch_dev is: the launch below orders this call after the device's
+// previous call when that one ran on another stream.
+static hipError_t noalloc_order_begin(int device, hipStream_t s, bool* ordered) {
+  *ordered = false;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return e;
+  // Under graph capture the call is recorded, not run: its order against
+  // other streams is the caller's to set.
+  if (cap != hipStreamCaptureStatusNone) return hipSuccess;
+  if (g_scratch_stream[device] && g_scratch_stream[device] != s) {
+    e = hipStreamWaitEvent(s, g_scratch_done[device], 0);
+    if (e != hipSuccess) return e;
+  }
+  *ordered = true;
+  return hipSuccess;
+}
+
+static hipError_t noalloc_order_end(int device, hipStream_t s) {
+  hipError_t e = hipEventRecord(g_scratch_done[device], s);
+  if (e != hipSuccess) return e;
+  g_scratch_stream[device] = s;
   return hipSuccess;
 }
 
@@ -570,17 +605,24 @@ __global__ void cu_from_lengths_kernel(NoAllocLengths a, int* cu) {
 
 hipError_t launch_mean_pool_noalloc(int dtype, const void* hidden, int cols,
                                     const NoAllocLengths& lengths, int max_len, int l2,
-                                    float* out, void* scratch_dev, hipStream_t s) {
+                                    float* out, int device, void* scratch_dev, hipStream_t s) {
   if (lengths.n <= 0) return hipSuccess;
-  if (!scratch_dev) return hipErrorInvalidValue;
+  if (!scratch_dev || device < 0 || device >= kMaxDevices) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[device] != scratch_dev) return hipErrorInvalidValue;
+  bool ordered = false;
+  hipError_t e = noalloc_order_begin(device, s, &ordered);
+  if (e != hipSuccess) return e;
   int* cu = (int*)scratch_dev;
   float* partial = (float*)((char*)scratch_dev + kNoAllocCuBytes);
   hipLaunchKernelGGL(cu_from_lengths_kernel, dim3(1), dim3(64), 0, s, lengths, cu);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   // The same kernels as fl_mean_pool, so the results are identical bit for bit.
-  return launch_mean_pool_staged(dtype, hidden, cols, cu, lengths.n, max_len, l2, partial, out,
-                                 nullptr, kNoAllocRowsPerChunk, s, false);
+  e = launch_mean_pool_staged(dtype, hidden, cols, cu, lengths.n, max_len, l2, partial, out,
+                              nullptr, kNoAllocRowsPerChunk, s, false);
+  if (e != hipSuccess || !ordered) return e;
+  return noalloc_order_end(device, s);
 }
 
 hipError_t launch_gather_cls(int dtype, const void* hidden, int cols, const int* cu_seqlens,

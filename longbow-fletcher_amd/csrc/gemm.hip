@@ -1249,7 +1249,7 @@ static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
 // At 512 tokens that sends FFN-down (96 K steps, 3 column tiles) and O to the
 // few-row kernel and keeps FFN-up (96 units per 16 rows) on the four-wave one.
 static bool gemm_small_better(const GemmParams& p) {
-  if (p.M > 4096) return false;
+  if (p.M > 4096 || !p.epi.allow_small) return false;
   const double nk = p.K / 32;
   const double units = (double)((p.M + 15) / 16) * (p.N / 64);
   const double small_us = units * nk * (p.epi.a_tiled ? 0.25e-3 : 0.6e-3) + 9.0;

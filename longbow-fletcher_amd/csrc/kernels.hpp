@@ -100,6 +100,11 @@ struct GemmEpilogue {
   // must be copies of row M-1 (true of row-major A, which is read clamped,
   // and of a tiled output written by an out_tiled GEMM from such an A).
   bool c_padded = false;
+  // The few-row kernel may take this GEMM (when its cost model says so).  It
+  // never writes output rows past M, so a consumer that relies on the padding
+  // rows of a tiled output being copies of row M-1 (a four-wave GEMM reading
+  // it with a_tiled and without c_padded) needs this off.
+  bool allow_small = true;
 };
 
 // Element offset of (row m, column k) of an activation matrix with K columns
@@ -250,9 +255,12 @@ struct NoAllocLengths {
 // Address of the current device's scratch array (`device` must be current);
 // looked up once per device and kept.
 hipError_t noalloc_scratch(int device, void** out);
+// Calls on one device from different streams run in call order (each waits
+// for the previous call's kernels when that call used another stream),
+// except under graph capture.
 hipError_t launch_mean_pool_noalloc(int dtype, const void* hidden, int cols,
                                     const NoAllocLengths& lengths, int max_len, int l2,
-                                    float* out, void* scratch_dev, hipStream_t s);
+                                    float* out, int device, void* scratch_dev, hipStream_t s);
 // out[r, c] = silu(in[r, c]) * in[r, inter + c] over an unfused [rows, 2*inter] product.
 hipError_t launch_swiglu(int dtype, const void* in, int rows, int inter, void* out, int math,
                          hipStream_t s);

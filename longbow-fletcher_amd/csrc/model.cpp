@@ -170,6 +170,9 @@ struct fl_model {
   // as well, so the O projection streams it in contiguous 16 KB blocks.
   bool ctx_tiled = false;
 
+  // The lane whose activations hold the most recent forward (fl_model_last_hidden).
+  int last_lane = 0;
+
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;
   size_t ev_next = 0;
@@ -341,6 +344,20 @@ int ensure_capacity(fl_model* m, Lane& L, int64_t T, int nseq, size_t nwork, siz
   return FL_OK;
 }
 
+// Frees a lane's activation buffers (the lane reallocates them on its next use).
+void release_activations(fl_model* m, Lane& L) {
+  if (L.stream) (void)hipStreamSynchronize(L.stream);
+  L.cap_tokens = 0;
+  L.last_lengths.clear();
+  untrack_free(m, L.X);
+  untrack_free(m, L.QKV);
+  untrack_free(m, L.CTX);
+  untrack_free(m, L.TMP);
+  untrack_free(m, L.G2);
+  untrack_free(m, L.ids32);
+  untrack_free(m, L.pos32);
+}
+
 constexpr int kPoolRows = 64;
 
 // Uploads cu_seqlens, per-token positions and the attention work list when
@@ -453,6 +470,7 @@ int gemm(fl_model* m, const Lane& L, bool mfma, const void* A, const void* W, vo
 // The forward on device-resident ids (L.ids32 or caller memory) into d_out, on L's stream.
 int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* flags) {
   hipStream_t s = L.stream;
+  m->last_lane = (int)(&L - m->lane);
   const int64_t T = L.T;
   const int H = m->H, dt = m->dtype;
   const int Ti = (int)T;
@@ -533,6 +551,11 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
           e.kind = EPI_SWIGLU;
           e.out_tiled = m->ffn_tiled;
           e.a_tiled = m->x_tiled;
+          // FFN-down reads this output tiled; without x_tiled it does not
+          // write its own padding rows (c_padded), so those rows of the
+          // output must be copies of row T-1, which only the four-wave
+          // kernel writes.
+          e.allow_small = !(m->ffn_tiled && !m->x_tiled);
           M_ST(gemm(m, L, true, L.X, w.wi, L.QKV, Ti, m->Ni, H, e));
         } else {
           // Unfused: [T, 2I] product, then silu(gate) * up into QKV.
@@ -992,26 +1015,32 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
   for (int64_t t = 0; t < tok; ++t)
     if (ids[t] < 0 || ids[t] >= m->cfg.vocab_size)  // cpu_backend.go:500-502
       return fail(FL_ERR_INVALID, "Gather index out of bounds");
-  // Forwards: runs of consecutive batches of at most kGroupTokens tokens
-  // (at least one batch each).
+  // Forwards: runs of consecutive batches of at most `cap` tokens (at least
+  // one batch each).
   struct Group { int b0, nb; };
   std::vector<Group> groups;
   int64_t max_gt = 0;
   int max_gs = 0;
-  for (int b = 0; b < (int)plan.size();) {
-    Group g{b, 0};
-    int64_t gt = 0;
-    int gs = 0;
-    while (b < (int)plan.size() && (g.nb == 0 || gt + plan[(size_t)b].tokens <= kGroupTokens)) {
-      gt += plan[(size_t)b].tokens;
-      gs += plan[(size_t)b].count;
-      ++g.nb;
-      ++b;
+  auto make_groups = [&](int64_t cap) {
+    groups.clear();
+    max_gt = 0;
+    max_gs = 0;
+    for (int b = 0; b < (int)plan.size();) {
+      Group g{b, 0};
+      int64_t gt = 0;
+      int gs = 0;
+      while (b < (int)plan.size() && (g.nb == 0 || gt + plan[(size_t)b].tokens <= cap)) {
+        gt += plan[(size_t)b].tokens;
+        gs += plan[(size_t)b].count;
+        ++g.nb;
+        ++b;
+      }
+      groups.push_back(g);
+      max_gt = std::max(max_gt, gt);
+      max_gs = std::max(max_gs, gs);
     }
-    groups.push_back(g);
-    max_gt = std::max(max_gt, gt);
-    max_gs = std::max(max_gs, gs);
-  }
+  };
+  make_groups(kGroupTokens);
 
   fl_model::Pipe& P = m->pipe;
   Lane& L0 = lane0(m);
@@ -1023,6 +1052,23 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     for (int k = 0; k < kLanes; ++k)
       if (!P.d2h[k]) M_CHECK(hipEventCreateWithFlags(&P.d2h[k], hipEventDisableTiming));
     P.ready = true;
+  }
+  // Every lane's activation buffers, sized for the largest forward, before
+  // anything is enqueued (Nomic fp16: ~1.1 GB per lane for 65536 tokens).
+  // When the device cannot hold them: one forward per batch of the plan, all
+  // on lane 0 (the context stream), as the reference computes them.
+  int nl = std::min<int>(kLanes, (int)groups.size());
+  {
+    int st = FL_OK;
+    for (int k = 0; k < nl && st == FL_OK; ++k)
+      st = ensure_capacity(m, m->lane[k], max_gt, max_gs, 1, 0);
+    if (st == FL_ERR_OOM && groups.size() < plan.size()) {
+      for (int k = 1; k < kLanes; ++k) release_activations(m, m->lane[k]);
+      make_groups(0);
+      nl = 1;
+      st = ensure_capacity(m, L0, max_gt, max_gs, 1, 0);
+    }
+    M_ST(st);
   }
   if (max_gt > P.cap_tok || max_gs > P.cap_seq) {
     for (int k = 0; k < kLanes; ++k) M_CHECK(hipStreamSynchronize(m->lane[k].stream));
@@ -1061,7 +1107,7 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     P.cap_seq = cq;
   }
 
-  // Forward f uses slot and lane f % kLanes: consecutive forwards compute on
+  // Forward f uses slot and lane f % nl: consecutive forwards compute on
   // the lanes' streams at the same time, each filling the CUs the others'
   // kernels leave idle.  A lane's stream carries its forward's upload,
   // kernels and download in order.  The host fills a slot's pinned ids only
@@ -1085,7 +1131,7 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     const Group& g = groups[(size_t)f];
     const Batch& p0 = plan[(size_t)g.b0];
     const Batch& pl = plan[(size_t)(g.b0 + g.nb - 1)];
-    const int k = f % kLanes;
+    const int k = f % nl;
     M_CHECK(hipEventSynchronize(P.d2h[k]));
     std::memcpy((char*)out + (size_t)p0.first * H * osz, P.out_pin[k],
                 (size_t)(pl.first + pl.count - p0.first) * H * osz);
@@ -1103,8 +1149,8 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     const Batch& pl = plan[(size_t)(g.b0 + g.nb - 1)];
     const int count = pl.first + pl.count - p0.first;
     const int64_t tokens = pl.tok0 + pl.tokens - p0.tok0;
-    const int k = f % kLanes;
-    if (f >= kLanes) M_ST(drain(f - kLanes));
+    const int k = f % nl;
+    if (f >= nl) M_ST(drain(f - nl));
     for (int64_t t = 0; t < tokens; ++t) P.ids_pin[k][t] = (int32_t)ids[p0.tok0 + t];
     Lane& L = m->lane[k];
     M_CHECK(hipMemcpyAsync(P.ids_dev[k], P.ids_pin[k], (size_t)tokens * 4, hipMemcpyHostToDevice,
@@ -1127,10 +1173,10 @@ int fl_model_embed_ex(fl_model* m, const int64_t* ids, const int64_t* lengths, i
     M_CHECK(hipMemcpyAsync(P.flags_pin[k], P.flags_dev[k], 8, hipMemcpyDeviceToHost, L.stream));
     M_CHECK(hipEventRecord(P.d2h[k], L.stream));
   }
-  for (int f = std::max(0, nf - kLanes); f < nf; ++f) M_ST(drain(f));
+  for (int f = std::max(0, nf - nl); f < nf; ++f) M_ST(drain(f));
   // fl_model_status then reports the last batch (drained, so its forward is done).
   const Group& gl = groups.back();
-  const int kl = (nf - 1) % kLanes;
+  const int kl = (nf - 1) % nl;
   if (gl.nb == 1) {
     M_CHECK(hipMemcpyAsync(L0.flags, P.flags_dev[kl], 8, hipMemcpyDeviceToDevice, cs));
   } else {
@@ -1158,8 +1204,12 @@ int fl_model_last_hidden(fl_model* m, float* out, int64_t n) {
   if (!m || !out) return fail(FL_ERR_INVALID, "null argument");
   std::lock_guard<std::recursive_mutex> lk(m->ctx->mu);
   M_ST(activate(m->ctx));
-  const Lane& L = lane0(m);
+  lane0(m);
+  // The lane of the most recent forward (fl_model_embed runs forward f on
+  // lane f % kLanes); its stream has finished before the copies below read it.
+  const Lane& L = m->lane[m->last_lane];
   if (n != L.T * m->H) return fail(FL_ERR_INVALID, "size mismatch");
+  M_CHECK(hipStreamSynchronize(L.stream));
   int st;
   // fp32 copy, then (X tiled) the row-major fp16 rows just past it.
   void* tmp = workspace(m->ctx, (size_t)n * 4 + (m->x_tiled ? (size_t)n * m->esz : 0), &st);

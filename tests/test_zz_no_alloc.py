@@ -3,10 +3,21 @@ callers that cannot allocate device memory) against fl_mean_pool, the entry
 point it is a variant of.  Both run the same kernels, so the outputs must be
 equal bit for bit, on two calls in a row, the second with a smaller input
 (the static scratch array keeps the first call's contents)."""
+import ctypes
+
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+
+
+def device_free_bytes():
+    """hipMemGetInfo's free bytes of the current device (device 0, made
+    current on this thread by the library's entry points)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
 
 
 @pytest.mark.parametrize("dtype_name", ["F16", "F32"])
@@ -24,10 +35,14 @@ def test_noalloc_pool_matches_fl_mean_pool(ctx, fl, dtype_name):
         hid = ctx.tensor(x, dtype)
         want = ctx.mean_pool(hid, lengths, l2=l2)
         out = ctx.empty((lengths.size, cols), fl.F32)
+        ctx.synchronize()
         before = ctx.vram_usage()[0]
+        free0 = device_free_bytes()
         ctx.mean_pool(hid, lengths, l2=l2, out=out, noalloc=True)
         ctx.synchronize()
+        # Neither the library's count nor the device's free memory moves.
         assert ctx.vram_usage()[0] == before
+        assert device_free_bytes() == free0
         np.testing.assert_array_equal(out.numpy(), want.numpy())
         for t in (hid, want, out):
             t.free()
@@ -56,3 +71,34 @@ def test_noalloc_pool_limits(ctx, fl):
     assert not np.any(out.numpy())
     hid.free()
     out.free()
+
+
+def test_noalloc_pool_two_contexts_in_call_order(fl):
+    """Two contexts on one GPU share its scratch array: calls made one after
+    the other, without a host synchronisation between them, run in that
+    order (the second waits for the first's kernels), so each gets its own
+    result."""
+    rng = np.random.default_rng(9)
+    ca, cb = fl.Context(0), fl.Context(0)
+    ts = []
+    try:
+        la = np.array([512] * 64, np.int64)
+        lb = np.array([7, 300, 41], np.int64)
+        ha = ca.tensor(rng.standard_normal((int(la.sum()), 768)).astype(np.float32), fl.F16)
+        hb = cb.tensor(rng.standard_normal((int(lb.sum()), 768)).astype(np.float32), fl.F16)
+        wa, wb = ca.mean_pool(ha, la), cb.mean_pool(hb, lb)
+        oa, ob = ca.empty((la.size, 768), fl.F32), cb.empty((lb.size, 768), fl.F32)
+        ts = [(ca, t) for t in (ha, wa, oa)] + [(cb, t) for t in (hb, wb, ob)]
+        ca.synchronize()
+        cb.synchronize()
+        for _ in range(3):
+            ca.mean_pool(ha, la, out=oa, noalloc=True)
+            cb.mean_pool(hb, lb, out=ob, noalloc=True)
+            ca.mean_pool(ha, la, out=oa, noalloc=True)
+        np.testing.assert_array_equal(ob.numpy(), wb.numpy())
+        np.testing.assert_array_equal(oa.numpy(), wa.numpy())
+    finally:
+        for _, t in ts:
+            t.free()
+        ca.close()
+        cb.close()
