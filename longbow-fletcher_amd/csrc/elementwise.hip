@@ -129,6 +129,12 @@ __global__ void has_nan_kernel(const T* t, int64_t n, int* flag) {
   if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
 }
 
+// p[i] = v for i < n (a fill kernel: a captured graph replays it reliably,
+// where memset nodes have given wrong results on replays after the first).
+__global__ void fill_i32_kernel(int* p, int n, int v) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
+}
+
 // One wave per row of an fp32 [rows x cols] matrix: flags[r] = 1 if row r
 // holds a NaN or an infinity, else 0 (every row's flag is written).
 __global__ void row_nonfinite_kernel(const float* t, int rows, int cols, int* flags) {
@@ -443,6 +449,13 @@ hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStr
   if (n <= 0) return hipSuccess;
   FL_DISPATCH(dtype, T, hipLaunchKernelGGL(has_nan_kernel<T>, grid_for(n), dim3(256), 0, s,
                                            (const T*)t, n, flag));
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int* p, int n, int v, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256),
+                     0, s, p, n, v);
   return hipGetLastError();
 }
 

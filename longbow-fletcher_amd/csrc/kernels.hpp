@@ -227,6 +227,8 @@ hipError_t launch_activation(int dtype, void* t, int rows, int cols, int act, in
 hipError_t launch_cast(const void* src, int sdt, void* dst, int ddt, int64_t n, int truncate_ref,
                        hipStream_t s);
 hipError_t launch_has_nan(const void* t, int dtype, int64_t n, int* flag, hipStream_t s);
+// p[0 .. n) = v, as a kernel (graph-capture safe, unlike a memset node).
+hipError_t launch_fill_i32(int* p, int n, int v, hipStream_t s);
 // flags[r] = 1 if row r of fp32 t [rows x cols] holds a NaN or an infinity, else 0.
 hipError_t launch_row_nonfinite(const float* t, int rows, int cols, int* flags, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* table, int cols, const int* idx, int n,

@@ -66,6 +66,14 @@ struct Staging {
 // next forward, four gained nothing.
 // Lanes of fl_model_embed's batch pipeline (lane 0 is the context stream's).
 constexpr int kLanes = 3;
+// Synchronous forwards of up to this many tokens (fl_model_forward[_ex],
+// fl_model_forward_padded) replay a HIP graph of their kernels, captured the
+// first time a lengths vector is seen; at most kGraphCache graphs are kept
+// (least recently used dropped).  A short forward is ~86 kernels of a few
+// microseconds each, so launch overhead is a large share of it.
+constexpr int64_t kGraphTokens = 4096;
+constexpr size_t kGraphCache = 16;
+
 // fl_model_embed computes consecutive batches of its plan together, in
 // forwards of up to this many tokens (a batch larger than that alone).  A
 // sequence's vector does not depend on the other sequences of its forward,
@@ -172,6 +180,19 @@ struct fl_model {
 
   // The lane whose activations hold the most recent forward (fl_model_last_hidden).
   int last_lane = 0;
+
+  // Captured forwards of lane 0 (kGraphTokens): the launches bake in the
+  // lane's buffer and table addresses, so an entry is used only while they
+  // are unchanged.
+  struct FwdGraph {
+    std::vector<int64_t> lengths;
+    std::vector<const void*> addrs;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  std::vector<FwdGraph> graphs;
+  uint64_t graph_clock = 0;
+  bool graphs_on = true;
 
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;
@@ -474,7 +495,7 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
   const int64_t T = L.T;
   const int H = m->H, dt = m->dtype;
   const int Ti = (int)T;
-  M_CHECK(hipMemsetAsync(flags, 0, 8, s));
+  M_CHECK(launch_fill_i32(flags, 2, 0, s));
   {
     ProfScope ps(m, L, P_EMBED);
     M_CHECK(launch_embed_ln(dt, d_ids, m->rope ? nullptr : L.pos32, m->word,
@@ -599,6 +620,20 @@ int run(fl_model* m, Lane& L, const int* d_ids, int nseq, float* d_out, int* fla
     }
   }
   return FL_OK;
+}
+
+// Every device address run() bakes into lane L's launches.
+std::vector<const void*> lane_addrs(const fl_model* m, const Lane& L) {
+  return {L.X,     L.QKV,  L.CTX,  L.TMP,  L.G2,      L.ids32,     L.pos32, L.cu,
+          L.work,  L.part, L.cls,  L.out,  L.flags,   L.rope_cs,   L.rope_cs_q,
+          m->ctx->stream};
+}
+
+// Destroys every captured forward.
+void drop_graphs(fl_model* m) {
+  for (auto& g : m->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  m->graphs.clear();
 }
 
 // Lane 0 runs on the context stream (looked up at every entry: the context
@@ -767,6 +802,7 @@ int fl_model_free(fl_model* m) {
       for (Staging& sg : L.meta) free_staging(sg);
     for (int k = 1; k < kLanes; ++k)
       if (m->lane[k].stream) (void)hipStreamDestroy(m->lane[k].stream);
+    drop_graphs(m);
     free_owned(m);
     for (hipEvent_t e : m->ev_pool) (void)hipEventDestroy(e);
   }
@@ -889,6 +925,47 @@ int fl_model_set_weight(fl_model* m, const char* name, const float* data, int64_
 // ExtractBytes, embeddings.go:256-286), half the bytes over PCIe.
 static bool valid_out_dtype(int dt) { return dt == FL_F32 || dt == FL_F16; }
 
+// run() on lane 0 through the graph cache (kGraphTokens).
+static int run_graphed(fl_model* m, Lane& L, const int64_t* lengths, int nseq) {
+  hipStream_t s = L.stream;
+  if (!m->graphs_on || m->prof || L.T > kGraphTokens) return run(m, L, L.ids32, nseq, L.out, L.flags);
+  std::vector<const void*> addrs = lane_addrs(m, L);
+  fl_model::FwdGraph* hit = nullptr;
+  for (auto& g : m->graphs)
+    if ((int)g.lengths.size() == nseq && std::equal(g.lengths.begin(), g.lengths.end(), lengths) &&
+        g.addrs == addrs) {
+      hit = &g;
+      break;
+    }
+  if (!hit) {
+    M_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int st = run(m, L, L.ids32, nseq, L.out, L.flags);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &graph);
+    if (st || e != hipSuccess) {
+      if (graph) (void)hipGraphDestroy(graph);
+      if (st) return st;
+      return hip_fail(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ie != hipSuccess) return hip_fail(ie, "hipGraphInstantiate");
+    if (m->graphs.size() >= kGraphCache) {
+      auto lru = std::min_element(m->graphs.begin(), m->graphs.end(),
+                                  [](const auto& a, const auto& b) { return a.used < b.used; });
+      (void)hipGraphExecDestroy(lru->exec);
+      m->graphs.erase(lru);
+    }
+    m->graphs.push_back({std::vector<int64_t>(lengths, lengths + nseq), std::move(addrs), exec, 0});
+    hit = &m->graphs.back();
+  }
+  hit->used = ++m->graph_clock;
+  m->last_lane = 0;
+  M_CHECK(hipGraphLaunch(hit->exec, s));
+  return FL_OK;
+}
+
 static int forward_common(fl_model* m, const int64_t* ids, const int64_t* lengths, int nseq,
                           int out_dtype, void* out) {
   if (nseq <= 0) return FL_OK;
@@ -904,7 +981,7 @@ static int forward_common(fl_model* m, const int64_t* ids, const int64_t* length
   }
   hipStream_t s = m->ctx->stream;
   M_CHECK(hipMemcpyAsync(L.ids32, i32.data(), (size_t)T * 4, hipMemcpyHostToDevice, s));
-  M_ST(run(m, L, L.ids32, nseq, L.out, L.flags));
+  M_ST(run_graphed(m, L, lengths, nseq));
   const size_t n = (size_t)nseq * m->H;
   if (out_dtype == FL_F16) {
     M_CHECK(launch_cast(L.out, FL_F32, L.out16, FL_F16, (int64_t)n, 0, s));
