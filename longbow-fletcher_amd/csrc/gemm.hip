@@ -25,6 +25,12 @@ namespace fl {
 constexpr int kGroupM = 8;
 // Four-wave kernel: the next tile's first K step runs inside the epilogue.
 constexpr bool kW4Fuse = true;
+// Four-wave kernel, STORE epilogue: a partial last round of tiles runs as
+// half-width tiles on twice as many CUs, for K up to kW4HalfMaxK (BERT-base
+// at 32768 tokens: O 0.052 -> 0.050 ms, QKV 0.116 -> 0.112; at K = 3072,
+// FFN-down, no gain: a half tile loads the whole tile's activations).
+constexpr bool kW4Half = true;
+constexpr int kW4HalfMaxK = 1024;
 // Direct-LDS 16-bit GEMM (plain layouts): K step, LDS stages (48 KB, two
 // workgroups per CU) and chunk swizzle (row >> 1) & 3.
 constexpr int kLdsBK = 32, kLdsStages = 2, kLdsSwz = 1;
@@ -649,7 +655,7 @@ __device__ __attribute__((always_inline)) inline void w4_dma(uint32_t lds_dst, u
 }
 
 template <typename T, int EPI, int MATH, int NS>
-__global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) {
+__global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles, int nhalf) {
   constexpr int BM = 256, BN = 256, BK = 32, ROWB = 64;
   constexpr int STAGE = (BM + BN) * ROWB;     // 32 KB
   constexpr int NLD = 8;                      // 1 KB loads per wave per step
@@ -666,14 +672,29 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
 
   const int G = (int)gridDim.x;
   const int me = xcd_remap((int)blockIdx.x, G);
-  const int my_tiles = me < ntiles ? (ntiles - 1 - me) / G + 1 : 0;
+  // Tiles ntiles .. ntiles + nhalf - 1 (STORE only) run as two 256x128
+  // halves each, on workgroups 0 .. 2 * nhalf - 1 after their full tiles
+  // (the host makes that the last, partial round): half tile me & 1 of tile
+  // ntiles + me / 2, both halves on one XCD.  A half tile loads the whole
+  // tile's K slices like a full one (the same DMA, waits and LDS layout), so
+  // the pipeline runs on across tiles unchanged; only its MFMAs, fragment
+  // reads (feature blocks 0-3 of its 128 weight rows) and epilogue are
+  // half-width.
+  constexpr bool HALF = EPI == EPI_STORE && MATH == MATH_EXACT;
+  const int my_full = me < ntiles ? (ntiles - 1 - me) / G + 1 : 0;
+  const bool has_half = HALF && me < 2 * nhalf;
+  const int my_tiles = my_full + (has_half ? 1 : 0);
   if (my_tiles == 0) return;
   const bool chunked = (ntiles % G == 0) && (G % 8 == 0);
   const int per = G / 8;
   const int num_m = (p.M + BM - 1) / BM, num_n = p.N / BN;
   const int per_group = GROUP_M * num_n;
-  auto coords = [&](int i, int& m0, int& n0) __attribute__((always_inline)) {
-    const int L = chunked ? (me / per) * (my_tiles * per) + i * per + (me % per) : i * G + me;
+  // Tile i of this workgroup: its 256x256 block and half (-1: the whole tile).
+  auto coords = [&](int i, int& m0, int& n0, int& hf) __attribute__((always_inline)) {
+    const bool h = has_half && i == my_full;
+    hf = h ? (me & 1) : -1;
+    const int L = h ? ntiles + (me >> 1)
+                    : chunked ? (me / per) * (my_full * per) + i * per + (me % per) : i * G + me;
     const int g = L / per_group;
     const int first_m = g * GROUP_M;
     const int gsize = min(num_m - first_m, GROUP_M);
@@ -682,6 +703,16 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     n0 = (r / gsize) * BN;
   };
   const int nk = p.K / BK;
+
+  // Fragment reads: A block t is rows 128*wm + 16t + (lane & 15), B block f
+  // rows 128*wn + 16f + (lane & 15), 16-byte k chunk lane >> 4 (swizzled).
+  const int fr = lane & 15, fg = lane >> 4;
+  const uint32_t co = (uint32_t)((fg ^ w4_swz<4>(fr)) << 4);
+  const uint32_t rdA = lds0 + (uint32_t)((wm * 128 + fr) * ROWB) + co;
+  const uint32_t rdB = lds0 + (uint32_t)(BM * ROWB + (wn * 128 + fr) * ROWB) + co;
+  // Half tiles: weight rows 128 * half + 64 * wn + 16f + (lane & 15), f < 4.
+  const uint32_t rdBh = lds0 + (uint32_t)(BM * ROWB + (wn * 64 + fr) * ROWB) + co;
+  const uint32_t dma0 = lds0 + (uint32_t)wave * 4096;
 
   // DMA geometry: wave w loads activation rows [64w, 64w+64) (loads 0-3) and
   // weight rows [64w, 64w+64) (loads 4-7) of each stage, 16 rows x 64 bytes
@@ -695,9 +726,11 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   constexpr size_t KB_STEP = (size_t)BN * BK * sizeof(T);  // one tiled weight block
   const bool a_tiled = p.epi.a_tiled;
   const size_t KA_STEP = a_tiled ? (size_t)BM * BK * sizeof(T) : BK * sizeof(T);
+  uint32_t rdBn = rdB;  // weight fragment base of the tile load_tile was given
   auto load_tile = [&](int ti) __attribute__((always_inline)) {
-    int m0, n0;
-    coords(ti, m0, n0);
+    int m0, n0, hf;
+    coords(ti, m0, n0, hf);
+    rdBn = hf < 0 ? rdB : rdBh + (uint32_t)(hf * 128 * ROWB);
     ka = a_tiled ? (const char*)p.A + (size_t)(m0 / BM) * nk * KA_STEP
                  : (const char*)p.A + (size_t)m0 * p.lda * sizeof(T);
     kb = (const char*)p.B + (size_t)(n0 / BN) * nk * KB_STEP;
@@ -712,14 +745,6 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     }
   };
 
-  // Fragment reads: A block t is rows 128*wm + 16t + (lane & 15), B block f
-  // rows 128*wn + 16f + (lane & 15), 16-byte k chunk lane >> 4 (swizzled).
-  const int fr = lane & 15, fg = lane >> 4;
-  const uint32_t co = (uint32_t)((fg ^ w4_swz<4>(fr)) << 4);
-  const uint32_t rdA = lds0 + (uint32_t)((wm * 128 + fr) * ROWB) + co;
-  const uint32_t rdB = lds0 + (uint32_t)(BM * ROWB + (wn * 128 + fr) * ROWB) + co;
-  const uint32_t dma0 = lds0 + (uint32_t)wave * 4096;
-
   // DMA of the cursor's step into stage st, then advance the cursor.
   auto load_step = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
@@ -733,6 +758,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // Prologue: steps 0 .. 3 into stages 0 .. 3; wait for steps 0 and 1;
   // fragments of step 0 into register set 0.
   load_tile(0);
+  uint32_t rdBc = rdBn;  // weight fragment base of the tile being multiplied
   if constexpr (EPI == EPI_ROPE) {
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) load_step(s);
@@ -742,7 +768,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     for (int s = 0; s < NS; ++s) load_step(s);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NLD) : "memory");
   }
-  asm volatile(FL_W4_READ_0 ::"v"(rdA), "v"(rdB) : "memory", FL_W4_CLOBBER_V);
+  asm volatile(FL_W4_READ_0 ::"v"(rdA), "v"(rdBc) : "memory", FL_W4_CLOBBER_V);
 
   // K step j of a group of four (global step s = j mod 4, since every tile
   // has a multiple of four steps): register set j % 2, reads stage (j+1)%4,
@@ -751,17 +777,30 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // A tile's first step (Z) loads nothing: its slice, step 3, went out
   // before the previous tile's epilogue, so that the next two steps' waits
   // can let the epilogue's stores stay outstanding.
-  auto kstep = [&](auto jc, auto zero, auto vmc) __attribute__((always_inline)) {
+  // H: a half tile's step (32 MFMAs, 12 fragment reads, the same loads).
+  // rdb: the weight fragment base of the tile whose next step is read (the
+  // next tile's in a tile's last step).
+  auto kstep = [&](auto jc, auto zero, auto vmc, auto hc, uint32_t rdb)
+                   __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
     constexpr int Z = decltype(zero)::value;  // 0 accumulate, 1 zero without DMA, 2 zero with DMA
     constexpr int VM = decltype(vmc)::value;
+    constexpr bool H = decltype(hc)::value;
     constexpr uint32_t RD = ((J + 1) % NS) * STAGE, DM = ((J + NS - 1) % NS) * STAGE;
 #define FL_W4_ARGS                                                                          \
-  ::"v"(rdA + RD), "v"(rdB + RD), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),        \
+  ::"v"(rdA + RD), "v"(rdb + RD), "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]),        \
       "v"(off[4]), "v"(off[5]), "v"(off[6]), "v"(off[7]), "s"(dma0 + DM), "s"(ka), "s"(kb),  \
       "n"(VM)                                                                              \
   : "memory", "m0", "scc", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A
-    if constexpr (F16T) {
+#define FL_W4_HCASE(j, z)                                                                   \
+  if constexpr (J % 2 == j && Z == z) {                                                    \
+    if constexpr (F16T) asm volatile(FL_W4_HSTEP_F16_##j##_##z FL_W4_ARGS);                 \
+    else asm volatile(FL_W4_HSTEP_BF16_##j##_##z FL_W4_ARGS);                               \
+  }
+    if constexpr (H) {
+      FL_W4_HCASE(0, 0) FL_W4_HCASE(0, 1) FL_W4_HCASE(0, 2)
+      FL_W4_HCASE(1, 0) FL_W4_HCASE(1, 1) FL_W4_HCASE(1, 2)
+    } else if constexpr (F16T) {
       if constexpr (J % 2 == 0 && Z == 0) asm volatile(FL_W4_STEP_F16_0_0 FL_W4_ARGS);
       if constexpr (J % 2 == 0 && Z == 1) asm volatile(FL_W4_STEP_F16_0_1 FL_W4_ARGS);
       if constexpr (J % 2 == 0 && Z == 2) asm volatile(FL_W4_STEP_F16_0_2 FL_W4_ARGS);
@@ -776,6 +815,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
       if constexpr (J % 2 == 1 && Z == 1) asm volatile(FL_W4_STEP_BF16_1_1 FL_W4_ARGS);
       if constexpr (J % 2 == 1 && Z == 2) asm volatile(FL_W4_STEP_BF16_1_2 FL_W4_ARGS);
     }
+#undef FL_W4_HCASE
 #undef FL_W4_ARGS
     if constexpr (Z != 1) {
       ka += KA_STEP;
@@ -802,7 +842,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
                : "=&v"(x[0]), "=&v"(x[1]), "=&v"(x[2]), "=&v"(x[3]), "=&v"(x[4]), "=&v"(x[5]), \
                  "=&v"(x[6]), "=&v"(x[7]), "=&v"(x[8]), "=&v"(x[9]), "=&v"(x[10]),           \
                  "=&v"(x[11]), "=&v"(x[12]), "=&v"(x[13]), "=&v"(x[14]), "=&v"(x[15])        \
-               : "v"(rdA + RD1), "v"(rdB + RD1)                                            \
+               : "v"(rdA + RD1), "v"(rdBn + RD1)                                           \
                : "memory", FL_W4_CLOBBER_V, FL_W4_CLOBBER_A)
 #define FL_W4_FUSED_CASE(t, h)                                                              \
   if constexpr (TB == t && HB == h) {                                                       \
@@ -840,8 +880,8 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   // exact only on straight-line code.)
   auto epilogue_hb = [&](int ti, auto hbc) __attribute__((always_inline)) {
     constexpr bool HB = decltype(hbc)::value;
-    int m0, n0;
-    coords(ti, m0, n0);
+    int m0, n0, hf;
+    coords(ti, m0, n0, hf);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     // The last MFMAs' results must be written before they are read.
@@ -1007,6 +1047,66 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
     else epilogue_hb(ti, std::false_type{});
   };
 
+  // Half tile (STORE, always a workgroup's last tile): the STORE epilogue
+  // over the wave's 128 x 64 block, accumulator tiles 8f + t, f < 4.  Unit t
+  // (16 rows of 128 bytes) is assembled in LDS buffer t % 2 and stored as
+  // whole rows while unit t+1 is computed.
+  auto epilogue_half = [&](int ti, auto hbc) __attribute__((always_inline)) {
+    constexpr bool HB = decltype(hbc)::value;
+    constexpr int HRB = 128, HCP = HRB / 16;
+    int m0, n0, hf;
+    coords(ti, m0, n0, hf);
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // The last MFMAs' results must be written before they are read.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    const int r = ln & 15, g = ln >> 4;
+    const int cbase = n0 + hf * 128 + wn * 64;  // the wave's first packed feature
+    char* stg = lds + NS * STAGE + wave * 8192;
+    const int mlast = p.epi.c_padded ? INT_MAX : p.M - 1;
+    float4_t bv[4];
+    if constexpr (HB) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) bv[f] = *(const float4_t*)(p.epi.bias + cbase + f * 16 + g * 4);
+    }
+    auto compute_unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int t = decltype(uc)::value;
+      char* buf = stg + (t & 1) * 2048;
+      auto put = [&](int col, float4_t a, float4_t b) __attribute__((always_inline)) {
+        const int c = (col - cbase) >> 3;
+        *(u32x4_t*)(buf + r * HRB + ((c ^ (r % HCP)) << 4)) = pack8<T>(a, b);
+      };
+      float4_t v[4];
+      v[0] = W4Acc<0 * 8 + t>::read();
+      v[1] = W4Acc<1 * 8 + t>::read();
+      v[2] = W4Acc<2 * 8 + t>::read();
+      v[3] = W4Acc<3 * 8 + t>::read();
+      w4_epilogue_block<T, EPI, MATH, HB>(
+          p, v, cbase, ln, [&](int f) { return bv[f]; },
+          [&](int) { return float4_t{0.f, 0.f, 0.f, 0.f}; }, put);
+    };
+    auto store_unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int t = decltype(uc)::value;
+      const char* buf = stg + (t & 1) * 2048;
+      const int c = ln % HCP;
+#pragma unroll
+      for (int k = 0; k < HCP / 4; ++k) {
+        const int rr = ln / HCP + k * (64 / HCP);
+        const u32x4_t val = *(const u32x4_t*)(buf + rr * HRB + ((c ^ (rr % HCP)) << 4));
+        const int m = min(m0 + wm * 128 + t * 16 + rr, mlast);
+        *(u32x4_t*)((T*)p.C + (size_t)m * p.ldc + cbase + c * 8) = val;
+      }
+    };
+    w4_for<8>([&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      compute_unit(uc);
+      if constexpr (u > 0) store_unit(std::integral_constant<int, u - 1>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    store_unit(std::integral_constant<int, 7>{});
+    asm volatile("" ::: "memory");
+  };
+
   // Per tile: group 0 (its first step multiplies into zero), groups 1 ..
   // G-2, and the last group, whose steps 1-3 load the next tile's steps 0-2
   // (past the last tile: its steps again, in bounds and never read).  Then
@@ -1030,34 +1130,49 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles) 
   using ZF = std::integral_constant<int, PRE3 ? 1 : 2>;
   using VM2 = std::conditional_t<PRE3, VME, VM8>;
   const int G4 = nk / 4;
-  for (int ti = 0; ti < my_tiles; ++ti) {
+  // Tile ti, full (hc false) or half.  Its last step reads the first
+  // fragments of the next tile (rdBn, set by load_tile); with FUSE, a full
+  // tile's epilogue runs the next tile's first step (a whole-width step
+  // also for a half tile: the extra accumulators are never read).
+  auto tile = [&](int ti, auto hc) __attribute__((always_inline)) {
+    using H = decltype(hc);
     // With FUSE, every tile but the first had its first step in the
     // previous epilogue.
-    if (!FUSE || ti == 0) kstep(I0{}, ZF{}, VM63{});
+    if (!FUSE || ti == 0) kstep(I0{}, ZF{}, VM63{}, H{}, rdBc);
     if (ti == 0) {
-      kstep(I1{}, Z0{}, VM8{});
-      kstep(I2{}, Z0{}, VM8{});
+      kstep(I1{}, Z0{}, VM8{}, H{}, rdBc);
+      kstep(I2{}, Z0{}, VM8{}, H{}, rdBc);
     } else {
-      kstep(I1{}, Z0{}, VME{});
-      kstep(I2{}, Z0{}, VM2{});
+      kstep(I1{}, Z0{}, VME{}, H{}, rdBc);
+      kstep(I2{}, Z0{}, VM2{}, H{}, rdBc);
     }
-    kstep(I3{}, Z0{}, VM8{});
+    kstep(I3{}, Z0{}, VM8{}, H{}, rdBc);
     for (int g = 1; g < G4 - 1; ++g) {
-      kstep(I0{}, Z0{}, VM8{});
-      kstep(I1{}, Z0{}, VM8{});
-      kstep(I2{}, Z0{}, VM8{});
-      kstep(I3{}, Z0{}, VM8{});
+      kstep(I0{}, Z0{}, VM8{}, H{}, rdBc);
+      kstep(I1{}, Z0{}, VM8{}, H{}, rdBc);
+      kstep(I2{}, Z0{}, VM8{}, H{}, rdBc);
+      kstep(I3{}, Z0{}, VM8{}, H{}, rdBc);
     }
-    kstep(I0{}, Z0{}, VM8{});
+    kstep(I0{}, Z0{}, VM8{}, H{}, rdBc);
     load_tile(ti + 1 < my_tiles ? ti + 1 : ti);
-    kstep(I1{}, Z0{}, VM8{});
-    kstep(I2{}, Z0{}, VM8{});
-    kstep(I3{}, Z0{}, VM8{});
+    kstep(I1{}, Z0{}, VM8{}, H{}, rdBc);
+    kstep(I2{}, Z0{}, VM8{}, H{}, rdBc);
+    kstep(I3{}, Z0{}, VM8{}, H{}, rdBn);
     // Steps 0 and 1 of the next tile have landed (step 1 is read in its
     // first step); step 3 goes out before the stores.
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NLD) : "memory");
     if constexpr (PRE3) load_step(3);
-    epilogue(ti);
+    if constexpr (H::value) {
+      if (p.epi.bias) epilogue_half(ti, std::true_type{});
+      else epilogue_half(ti, std::false_type{});
+    } else {
+      epilogue(ti);
+    }
+    rdBc = rdBn;
+  };
+  for (int ti = 0; ti < my_full; ++ti) tile(ti, std::false_type{});
+  if constexpr (HALF) {
+    if (has_half) tile(my_full, std::true_type{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -1234,9 +1349,23 @@ static bool gemm_w4_ok(const GemmParams& p) {
 template <typename T, int EPI, int MATH>
 static hipError_t launch_w4(const GemmParams& p, hipStream_t s) {
   const int ntiles = ((p.M + 255) / 256) * (p.N / 256);
+  // STORE: a partial last round on at most half the CUs runs as half tiles,
+  // two per tile, on twice as many (the kernel's nhalf).  The full rounds
+  // take every CU (full is a multiple of the CU count), so each workgroup
+  // has the same number of full tiles and 2 * rest <= grid.
+  const int cus = cu_count();
+  const int rest = ntiles % cus;
+  if (EPI == EPI_STORE && MATH == MATH_EXACT && kW4Half && p.K <= kW4HalfMaxK && rest > 0 &&
+      2 * rest <= cus) {
+    const int full = ntiles - rest;
+    const int grid = full > 0 ? persistent_grid(full) : 2 * rest;
+    hipLaunchKernelGGL((gemm_w4_kernel<T, EPI, MATH, 4>), dim3(grid), dim3(256), 0, s, p, full,
+                       rest);
+    return hipGetLastError();
+  }
   const int grid = persistent_grid(ntiles);
   hipLaunchKernelGGL((gemm_w4_kernel<T, EPI, MATH, 4>), dim3(grid), dim3(256), 0, s,
-                     p, ntiles);
+                     p, ntiles, 0);
   return hipGetLastError();
 }
 

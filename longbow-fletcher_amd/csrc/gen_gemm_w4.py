@@ -23,6 +23,9 @@ feature fragment 0 in the stage being read, %2..%9 the lanes' global byte
 offsets of the 8 loads, %10 the LDS address of the wave's first load, %11 /
 %12 the 64-bit token / weight base of the loaded K slice, %13 the vmcnt.
 
+FL_W4_HSTEP_*: the step of a half-width tile (step_hf), with the same
+operands and zero variants.
+
 Run: python gen_gemm_w4.py  (rewrites gemm_w4.inc next to this file).
 """
 import pathlib
@@ -90,6 +93,37 @@ def fused_half(dtype, t, half):
     return out
 
 
+# Half-width step (a tile's last-round half, HALF_DMA_AFTER / step_hf): the
+# full register map and the full step's DMA loads, operands and wait, but
+# only feature blocks 0-3: 32 MFMAs (token block major) and 12 fragment reads
+# of the next step (token blocks 0-7, feature blocks 0-3).
+HALF_READ_AFTER = [(32 * r) // 12 for r in range(12)]
+HALF_DMA_AFTER = [4 * j + 2 for j in range(8)]
+
+
+def step_hf(dtype, cur, zero):
+    rc = 128 + 64 * cur
+    rn = 128 + 64 * (1 - cur)
+    out = ["s_waitcnt vmcnt(%13)", "s_waitcnt lgkmcnt(0)", "s_barrier"]
+    for i in range(32):
+        t, f = i >> 2, i & 3
+        k = 8 * f + t
+        acc = f"a[{4 * k}:{4 * k + 3}]"
+        src_c = "0" if zero else acc
+        out.append(f"{MNEMONIC[dtype]} {acc}, {vreg(rc + 32 + 4 * f)}, {vreg(rc + 4 * t)}, {src_c}")
+        for r in (r for r in range(12) if HALF_READ_AFTER[r] == i):
+            if r < 8:
+                out.append(f"ds_read_b128 {vreg(rn + 4 * r)}, %0 offset:{r * 1024}")
+            else:
+                out.append(f"ds_read_b128 {vreg(rn + 32 + 4 * (r - 8))}, %1 offset:{(r - 8) * 1024}")
+        for j in (j for j in range(8) if HALF_DMA_AFTER[j] == i and zero != 1):
+            imm = j * 1024 if j < 4 else 16384 + (j - 4) * 1024
+            out.append("s_mov_b32 m0, %10" if imm == 0 else f"s_add_u32 m0, %10, {imm}")
+            out.append("s_nop 0")
+            out.append(f"global_load_lds_dwordx4 %{2 + j}, {'%11' if j < 4 else '%12'}")
+    return out
+
+
 def reads(cur):
     r0 = 128 + 64 * cur
     out = []
@@ -129,6 +163,12 @@ def generate(**kw):
     parts.append("#define FL_W4_READ_0 \\")
     parts.append(as_c_string(reads(0)))
     parts.append("")
+    for dtype in ("F16", "BF16"):
+        for cur in (0, 1):
+            for zero in (0, 1, 2):
+                parts.append(f"#define FL_W4_HSTEP_{dtype}_{cur}_{zero} \\")
+                parts.append(as_c_string(step_hf(dtype, cur, zero)))
+                parts.append("")
     # Accumulator tile k -> four floats, for the epilogue.
     parts.append("template <int K> struct W4Acc;")
     for k in range(64):

@@ -29,8 +29,9 @@ def test_generated_include_is_current():
     assert (CSRC / "gemm_w4.inc").read_text() == gen_gemm_w4.generate()
 
 
-def _kernels(asm: str):
-    for m in re.finditer(r"^(_ZN2fl14gemm_w4_kernel\S*):.*?$(.*?)^\.Lfunc_end", asm, re.M | re.S):
+def _kernels(asm: str, name: str = "gemm_w4_kernel"):
+    pat = r"^(_ZN2fl%d%s\S*):.*?$(.*?)^\.Lfunc_end" % (len(name), name)
+    for m in re.finditer(pat, asm, re.M | re.S):
         meta = re.search(r"\.amdhsa_kernel " + re.escape(m.group(1)) + r"(.*?)\.end_amdhsa_kernel",
                          asm, re.S).group(1)
         yield m.group(1), m.group(2), meta
@@ -49,22 +50,31 @@ def _compiler_lines(body: str):
                 yield code
 
 
-def test_w4_kernel_register_discipline(tmp_path):
+@pytest.fixture(scope="module")
+def gemm_asm(tmp_path_factory):
     import longbow_fletcher_amd.build as B
     if not shutil.which(B.HIPCC) and not pathlib.Path(B.HIPCC).exists():
         pytest.skip("hipcc not available")
-    out = tmp_path / "gemm.s"
+    out = tmp_path_factory.mktemp("asm") / "gemm.s"
     cmd = [B.HIPCC, *B.COMMON, f"-I{CSRC}", *B.PER_FILE.get("gemm.hip", []), "--cuda-device-only",
            "-S", "-o", str(out), str(CSRC / "gemm.hip")]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-3000:]
-    asm = out.read_text()
+    return out.read_text()
+
+
+def test_w4_kernel_register_discipline(gemm_asm):
+    asm = gemm_asm
     found = 0
     for name, body, meta in _kernels(asm):
         found += 1
         assert re.search(r"\.amdhsa_private_segment_fixed_size 0\b", meta), f"{name} spills"
         assert re.search(r"\.amdhsa_accum_offset 256\b", meta), name
-        assert len(re.findall(r"v_mfma_f32_16x16x32_(?:f16|bf16)", body)) >= 512, name
+        mfmas = len(re.findall(r"v_mfma_f32_16x16x32_(?:f16|bf16)", body))
+        assert mfmas >= 512, name
+        if "_Li0ELi1E" in name:
+            # STORE also has the half-tile steps (12 blocks of 32 MFMAs).
+            assert mfmas >= 512 + 384, (name, mfmas)
         bad = []
         for code in _compiler_lines(body):
             if re.search(r"\bm0\b", code) or "scratch_" in code:
