@@ -21,8 +21,14 @@ namespace fl {
 
 // Tuning constants, chosen by measurement on MI355X.
 // Row blocks per group of the persistent tile order (an XCD's workgroups
-// share a group's activation rows in L2).
+// share a group's activation rows in L2).  Outputs of at most
+// kGroupNarrowN column tiles go column-fastest instead (groups of one row
+// block): an XCD's 32 workgroups then take about 11 whole row blocks per
+// round, where groups of 8 row blocks x 3 column tiles split a third of the
+// blocks between rounds and fetch them twice (Nomic at 131072 tokens:
+// FFN-down 1458 -> 1099 MB per launch, O 370 -> 280 MB; times unchanged).
 constexpr int kGroupM = 8;
+constexpr int kGroupNarrowN = 4;
 // Four-wave kernel: the next tile's first K step runs inside the epilogue.
 constexpr bool kW4Fuse = true;
 // Four-wave kernel, STORE epilogue: a partial last round of tiles runs as
@@ -659,7 +665,7 @@ __global__ void __launch_bounds__(256) gemm_w4_kernel(GemmParams p, int ntiles, 
   constexpr int BM = 256, BN = 256, BK = 32, ROWB = 64;
   constexpr int STAGE = (BM + BN) * ROWB;     // 32 KB
   constexpr int NLD = 8;                      // 1 KB loads per wave per step
-  constexpr int GROUP_M = kGroupM;
+  const int GROUP_M = p.N / BN <= kGroupNarrowN ? 1 : kGroupM;
   constexpr bool F16T = Elem<T>::dtype == F16;
   static_assert(NS == 4, "the K loop runs in groups of four steps, one per stage");
   // NS stages, then an 8 KB epilogue staging area per wave.
